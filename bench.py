@@ -1,0 +1,233 @@
+"""HOFA hot-path benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 4] [--skip-cpu]
+
+A step is one pass of the hot path over one batch of synthetic input: one
+decode token of the BASELINE cfg3 workload (H=16, d_h=64, r=16, 32768-row bf16
+outlier cache, fp32 48x64 GLA state per head) for B sequences.  The headline
+``value`` is decode tokens/s at B=4; B=1 is reported beside it.
+
+Every step reads a different cache set from a rotation whose total size is at
+least 1 GiB, so the timed steps stream from HBM instead of the 256 MB
+last-level cache.  The K timed steps are replayed from captured HIP graphs and
+bracketed by HIP events on the stream the kernels run on.
+
+The CPU baseline times the build's own PyTorch restatement of the reference
+path (``oracle/hofa_ref.py``; kind "port") on a bounded sample of the same
+workload on this host.
+
+Prints ONE JSON line (rank 0).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+import torch.nn.functional as F
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor figure
+MFMA_BF16_PEAK_TFS = 2500.0    # MI355X dense bf16 MFMA, vendor figure
+
+H, D, R, L = 16, 64, 16, 32768
+J = D - R
+
+
+def decode_bytes(B: int) -> int:
+    """Algorithmic HBM bytes of one decode step: both caches once, the fp32
+    state read and written, plus q/k/v/y and the per-head scalars."""
+    cache = B * H * L * (R + D) * 2
+    state = B * H * J * D * 4 * 2
+    small = B * H * (4 * D * 2 + 3 * 4) + H * D * 4
+    return cache + state + small
+
+
+def make_decode_set(B: int, gen: torch.Generator, dev="cuda"):
+    f = dict(dtype=torch.float32)
+    qkv = torch.randn(B, 1, H, 3 * D, generator=gen, **f).to(dev, torch.bfloat16)
+    q, k, v = (qkv[..., i * D:(i + 1) * D].transpose(1, 2) for i in range(3))
+    ck = torch.randn(B, H, L, R, generator=gen, **f).to(dev, torch.bfloat16)
+    cv = torch.randn(B, H, L, D, generator=gen, **f).to(dev, torch.bfloat16)
+    s_in = (0.1 * torch.randn(B, H, J, D, generator=gen, **f)).to(dev)
+    s_out = torch.empty_like(s_in)
+    lg = torch.clamp(F.logsigmoid(torch.randn(B, H, 1, generator=gen, **f)) / 16, -5, 0).to(dev)
+    mix = torch.sigmoid(torch.randn(B, H, 1, generator=gen, **f)).to(dev)
+    nw = torch.ones(H, D, device=dev)
+    return dict(q=q, k=k, v=v, ck=ck, cv=cv, s_in=s_in, s_out=s_out, lg=lg, mix=mix, nw=nw)
+
+
+def _decode_call(st):
+    from outlierneuronattention_amd import fused_hofa_decode
+    return fused_hofa_decode(st["q"], st["k"], st["v"], st["ck"], st["cv"], st["s_in"], st["s_out"], st["lg"],
+                             st["mix"], st["nw"], R, L, math.sqrt(D / R))
+
+
+def bench_decode(B: int, steps: int, warmup: int, rotate_bytes: int = 1 << 30):
+    gen = torch.Generator().manual_seed(1234 + B)
+    nbuf = max(1, math.ceil(rotate_bytes / decode_bytes(B)))
+    sets = [make_decode_set(B, gen) for _ in range(nbuf)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(max(warmup, nbuf)):
+            _decode_call(sets[i % nbuf])
+        s.synchronize()
+        full = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(full, stream=s):
+            for st in sets:
+                _decode_call(st)
+        rem = steps % nbuf
+        part = None
+        if rem:
+            part = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(part, stream=s):
+                for st in sets[:rem]:
+                    _decode_call(st)
+        full.replay()
+        s.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(s)
+        for _ in range(steps // nbuf):
+            full.replay()
+        if part is not None:
+            part.replay()
+        t1.record(s)
+        torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1)
+    step_s = ms / 1e3 / steps
+    nbytes = decode_bytes(B)
+    return dict(B=B, ms_per_step=ms / steps, tok_per_s=B / step_s, bytes_per_step=nbytes,
+                gbs=nbytes / step_s / 1e9, rotation_sets=nbuf)
+
+
+def bench_decode_hot(B: int, steps: int):
+    """Same kernel on one cache set (last-level-cache resident when it fits)."""
+    gen = torch.Generator().manual_seed(99)
+    st = make_decode_set(B, gen)
+    for _ in range(3):
+        _decode_call(st)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _decode_call(st)
+        s.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(10):
+                _decode_call(st)
+        g.replay()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(s)
+        n = max(1, steps // 10)
+        for _ in range(n):
+            g.replay()
+        t1.record(s)
+        torch.cuda.synchronize()
+    step_s = t0.elapsed_time(t1) / 1e3 / (n * 10)
+    return dict(B=B, us_per_step=step_s * 1e6, gbs=decode_bytes(B) / step_s / 1e9)
+
+
+def cpu_baseline_decode(B: int, budget_s: float = 10.0):
+    """Oracle decode step (torch CPU fp32) on the cfg3 shape: time until the
+    budget is spent (at least 2 steps after one warm-up)."""
+    from oracle import hofa_ref as ref
+    gen = torch.Generator().manual_seed(5)
+    q = torch.randn(B, H, D, generator=gen)
+    k = torch.randn(B, H, D, generator=gen)
+    v = torch.randn(B, H, D, generator=gen)
+    ck = torch.randn(B, H, L, R, generator=gen)
+    cv = torch.randn(B, H, L, D, generator=gen)
+    st = 0.1 * torch.randn(B, H, J, D, generator=gen)
+    lg = F.logsigmoid(torch.randn(B, H, generator=gen)) / 16
+    mix = torch.sigmoid(torch.randn(B, H, generator=gen))
+    nw = torch.ones(H, D)
+    sm = math.sqrt(D / R)
+    ref.decode_step(q, k, v, ck, cv, L, st, lg, mix, nw, R, sm)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        ref.decode_step(q, k, v, ck, cv, L, st, lg, mix, nw, R, sm)
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= budget_s and n >= 2) or n >= 10000:
+            break
+    return dict(value=B * n / el, unit="tok/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{n} decode steps of cfg3 at B={B} (H=16, d_h=64, r=16, L=32768) in fp32, "
+                       f"oracle/hofa_ref.decode_step, {el:.1f} s")
+
+
+def _traffic_from_profile(name: str):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary, if present."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1])
+            except ValueError:
+                return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--batch", type=int, default=4, help="batch of the headline decode line")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the multi-GPU "
+              "layout is a design note, not a measured path.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    other = 1 if args.batch != 1 else 4
+    head = bench_decode(args.batch, args.steps, args.warmup)
+    side = bench_decode(other, args.steps, args.warmup)
+    hot = bench_decode_hot(1, min(args.steps, 500))
+    cpu = None if args.skip_cpu else cpu_baseline_decode(args.batch, args.cpu_budget)
+    achieved = head["gbs"]
+    line = {
+        "metric": "decode tok/s (split-K HOFA decode, 32k ctx)",
+        "value": round(head["tok_per_s"], 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) caches, N(0,0.1) fp32 state; random gates)",
+        "config": {"workload": "cfg3: split-K decode of one token, H=16 d_h=64 r=16, L=32768 bf16 cache, "
+                               "fp32 48x64 GLA state per head",
+                   "global_batch": args.batch, "seq_len": L, "parallelism": "none (1 GPU)",
+                   "rotation_sets": head["rotation_sets"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": _traffic_from_profile(f"decode_cfg3_B{args.batch}_pmc.txt")},
+        "cpu_baseline": cpu,
+        "decode": {f"B{head['B']}": {k: round(v, 4) if isinstance(v, float) else v for k, v in head.items()},
+                   f"B{side['B']}": {k: round(v, 4) if isinstance(v, float) else v for k, v in side.items()},
+                   "B1_llc_resident": {k: round(v, 3) if isinstance(v, float) else v for k, v in hot.items()}},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,109 @@
+/*
+ * hofa.h - C ABI of the MI355X (gfx950) HOFA hybrid-attention library.
+ *
+ * Plain pointers, sizes and element strides only: no framework types cross
+ * this boundary.  Every entry point enqueues work on the HIP stream passed as
+ * `stream` (a hipStream_t; NULL = the legacy default stream), returns 0 on
+ * success and a negative code on a rejected argument or a launch error;
+ * hofa_last_error() then describes the failure (thread-local string).
+ *
+ * Paths in comments are relative to the reference repository root.
+ */
+#ifndef HOFA_H
+#define HOFA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes. */
+enum { HOFA_F32 = 0, HOFA_BF16 = 1, HOFA_F16 = 2 };
+
+/* Error codes. */
+enum { HOFA_OK = 0, HOFA_EINVAL = -1, HOFA_EUNSUPPORTED = -2, HOFA_ELAUNCH = -3, HOFA_EWORKSPACE = -4 };
+
+/*
+ * A strided tensor view: base pointer, element type and element strides of
+ * up to four dimensions (unused trailing strides are ignored).  Sizes come
+ * from the scalar fields of the argument struct that holds the view.
+ */
+typedef struct {
+    const void *data;
+    int32_t dtype;
+    int32_t reserved;
+    int64_t stride[4];
+} hofa_view_t;
+
+/* ------------------------------------------------------------------------
+ * Split-K decode of one token.
+ *
+ * Replaces fused_hofa_decode(q, k, v, cache_k, cache_v, state_I_in,
+ * state_I_out, log_gamma, mix_g, norm_w, R, seq_len, sm_scale, split_k,
+ * log_alpha) (src/hofa_decode_triton.py:342-476) and the three Triton kernels
+ * behind it (:48-159, :173-239, :242-340).
+ *
+ *   outlier:  y_O = softmax(q[:R] . cache_k[0:seq_len]^T * sm_scale) cache_v[0:seq_len]
+ *   inlier:   S'  = gamma (.) S_in + k[R:]^T v ;  y_I = q[R:] S'
+ *             gamma_j = exp(log_gamma * exp(log_alpha[h, j]))  (exp(log_gamma) without alpha)
+ *   output:   y = mix * y_O + (1 - mix) * RMSNorm(y_I; eps) * norm_w[h]
+ *
+ * Views (element strides; q/k/v/cache/y share one dtype, f32 | bf16 | f16):
+ *   q, k, v    [B,H,1,D]       stride[0..3] = b, h, n, d
+ *   cache_k    [B,H,L,R]       stride[3] must be 1, rows 16-byte aligned
+ *   cache_v    [B,H,L,D]       stride[3] must be 1, rows 16-byte aligned
+ *   state_in   [B,H,J,D] f32   contiguous  (J = D - R)
+ *   state_out  [B,H,J,D] f32   contiguous, must not alias state_in
+ *   log_gamma  [B,H,1]         stride[0..1] = b, h  (f32 | bf16 | f16)
+ *   mix        [B,H,1]         stride[0..1] = b, h  (0 strides allowed)
+ *   norm_w     [H,D]           stride[0..1] = h, d
+ *   log_alpha  [H,J]           stride[0..1] = h, j; data NULL = no alpha
+ *   y          [B,H,1,D]       output
+ * seq_len rows of the caches are read (the new token already written at row
+ * seq_len-1).  When seq_len_dev is non-NULL the count is read on the device
+ * at run time (graph replay with an advancing position) and cache_len bounds
+ * it.  split_k = 0 chooses the split count from the CU count (at most 64).
+ * Supported: D in {64, 128}, R in {16, 32, 64}, 8*R >= D, R < D; one head's
+ * cache must span less than 2 GiB.  The call enqueues two kernels (cache
+ * streaming, then the per-head state update and merge).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    int32_t B, H, D, R;
+    int32_t seq_len;
+    int32_t cache_len;
+    const int32_t *seq_len_dev;
+    float sm_scale;
+    float eps;
+    int32_t split_k;
+    int32_t reserved;
+    hofa_view_t q, k, v;
+    hofa_view_t cache_k, cache_v;
+    hofa_view_t state_in, state_out;
+    hofa_view_t log_gamma, mix, norm_w, log_alpha;
+    hofa_view_t y;
+} hofa_decode_args_t;
+
+/* Bytes of scratch the call needs (depends on B, H, D and the split plan):
+ * one partial (m, l, acc[D]) per stream block.  No initialisation is needed;
+ * calls that share a buffer must be stream-ordered.  Returns 0 for rejected
+ * arguments. */
+size_t hofa_decode_workspace_bytes(const hofa_decode_args_t *args);
+
+/* No reference counterpart beyond the split choice at
+ * src/hofa_decode_triton.py:374-383: reports the split count and tokens per
+ * split the call would use. */
+int hofa_decode_plan(const hofa_decode_args_t *args, int32_t *split_k, int32_t *tokens_per_split);
+
+int hofa_decode(const hofa_decode_args_t *args, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Library-wide helpers. */
+const char *hofa_last_error(void);
+int hofa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HOFA_H */

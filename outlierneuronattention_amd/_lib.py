@@ -1,0 +1,140 @@
+"""ctypes binding to ``libhofa.so`` (the C ABI declared in ``include/hofa.h``).
+
+torch is imported first on purpose: its bundled HIP runtime is then the one
+the library binds to (same SONAME), so torch's streams and allocations are
+valid inside the library.  The library is required: there is no fallback, and
+every op raises if it is missing or was built for another GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libhofa.so")
+
+HOFA_F32, HOFA_BF16, HOFA_F16 = 0, 1, 2
+_DTYPE_CODE = {torch.float32: HOFA_F32, torch.bfloat16: HOFA_BF16, torch.float16: HOFA_F16}
+_ERRORS = {-1: "invalid argument", -2: "unsupported configuration", -3: "launch failure", -4: "workspace"}
+
+
+class HofaError(RuntimeError):
+    """Raised when the HIP library rejects a call or a launch fails."""
+
+
+class View(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("stride", ctypes.c_int64 * 4)]
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("H", ctypes.c_int32), ("D", ctypes.c_int32), ("R", ctypes.c_int32),
+                ("seq_len", ctypes.c_int32), ("cache_len", ctypes.c_int32),
+                ("seq_len_dev", ctypes.c_void_p),
+                ("sm_scale", ctypes.c_float), ("eps", ctypes.c_float),
+                ("split_k", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("q", View), ("k", View), ("v", View),
+                ("cache_k", View), ("cache_v", View),
+                ("state_in", View), ("state_out", View),
+                ("log_gamma", View), ("mix", View), ("norm_w", View), ("log_alpha", View),
+                ("y", View)]
+
+
+# (name, restype, argtypes) of every entry point declared in include/hofa.h
+EXPORTS = [
+    ("hofa_decode_workspace_bytes", ctypes.c_size_t, [ctypes.POINTER(DecodeArgs)]),
+    ("hofa_decode_plan", ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_int32),
+                                        ctypes.POINTER(ctypes.c_int32)]),
+    ("hofa_decode", ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    ("hofa_last_error", ctypes.c_char_p, []),
+    ("hofa_version", ctypes.c_int, []),
+]
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the library once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(path):
+                raise HofaError(f"HOFA HIP library not found at {path}; build it with "
+                                "`python -m outlierneuronattention_amd.build_lib`")
+            lib = ctypes.CDLL(path)
+            for name, res, args in EXPORTS:
+                fn = getattr(lib, name)
+                fn.restype, fn.argtypes = res, args
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().hofa_last_error().decode(errors="replace")
+        raise HofaError(f"{what} failed ({_ERRORS.get(rc, rc)}): {msg}")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise HofaError(f"unsupported dtype {t.dtype}") from None
+
+
+def view(t: torch.Tensor | None, strides=None) -> View:
+    """A ``hofa_view_t`` of ``t``; ``strides`` overrides ``t.stride()`` (element units)."""
+    v = View()
+    if t is None:
+        return v
+    v.data = t.data_ptr()
+    v.dtype = dtype_code(t)
+    st = list(t.stride() if strides is None else strides)
+    for i, s in enumerate(st[:4]):
+        v.stride[i] = int(s)
+    return v
+
+
+def require_gpu(*tensors: torch.Tensor) -> None:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise HofaError(f"HOFA ops run on the GPU only; got a tensor on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise HofaError(f"tensors on different devices: {dev} and {t.device}")
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class WorkspaceCache:
+    """Scratch buffers keyed by (device, stream, purpose).
+
+    One buffer per stream keeps concurrently running streams from sharing
+    scratch; a buffer only grows.  Allocate (warm up) before graph capture.
+    """
+
+    def __init__(self):
+        self._bufs: dict = {}
+
+    def get(self, device: torch.device, stream: int, tag: str, nbytes: int) -> torch.Tensor:
+        key = (device.index, stream, tag)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
+
+
+WORKSPACES = WorkspaceCache()

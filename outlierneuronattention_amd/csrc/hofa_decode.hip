@@ -1,0 +1,501 @@
+// Split-K HOFA decode for gfx950: two launches per token.
+//
+// Replaces fused_hofa_decode and its Triton kernels
+// (src/hofa_decode_triton.py:173-239 split, :242-340 reduce, host :342-476).
+//
+// 1. stream kernel, grid B*H + B*H*n_split, 256 threads.  The first B*H
+//    blocks apply the GLA update S' = gamma (.) S + k_I^T v to one head's
+//    [J, D] fp32 state (float4 rows) and write y_I = q_I S'.  Every other
+//    block (head, split) runs an online softmax over cache rows
+//    [split*tps, (split+1)*tps) of one head.
+//    Each wave owns a quarter of the range; rows are fetched as 16-byte buffer
+//    loads (a tile of TT tokens is eight V vectors per lane, LPR lanes per V
+//    row, plus 8R/D K vectors per lane, KL lanes per K row) and the next tile
+//    is in flight while the current one is consumed.  Rows at or beyond the
+//    valid length read as zero through the buffer range check and get a -inf
+//    score.  The four waves merge in LDS and the block writes one partial
+//    (m, l, acc[D]) in the base-2 log domain.
+//    The state block also finishes the inlier side,
+//    z = (1 - mix) * RMSNorm(y_I) * norm_w, and stores z and mix.
+// 2. merge kernel, grid B*H, one wave per head: loads the partials in batches
+//    issued before use, merges them by log-sum-exp and writes
+//    y = mix * y_O + z.
+// The kernel boundary orders the partial writes before the merge's reads, so
+// no device-scope fence or counter is needed and the workspace carries no
+// state between calls.
+#include "hofa_common.h"
+
+namespace hofa {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxSplit = 64;  // partials merged per head (one per lane of the merge wave)
+constexpr int kBufFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+constexpr int kLoadNT = 2;             // non-temporal hint for streamed cache rows
+
+struct DecodeKArgs {
+    const void *q, *k, *v, *cache_k, *cache_v;
+    const float *state_in;
+    float *state_out;
+    const void *log_gamma, *mix, *norm_w, *log_alpha;
+    void *y;
+    const int32_t *seq_len_dev;
+    float *ws_acc;  // [B*H][n_split][D] partial numerators
+    float *ws_ml;   // [B*H][n_split][2] partial (max, denominator), base-2 domain
+    float *ws_z;    // [B*H][D + 4] inlier contribution and mix
+    int64_t q_sb, q_sh, q_sd, k_sb, k_sh, k_sd, v_sb, v_sh, v_sd;
+    int64_t ck_sb, ck_sh, ck_sl, cv_sb, cv_sh, cv_sl;
+    int64_t st_sb, st_sh, so_sb, so_sh;
+    int64_t lg_sb, lg_sh, mg_sb, mg_sh, nw_sh, nw_sd, la_sh, la_sj;
+    int64_t y_sb, y_sh, y_sd;
+    int lg_dt, mg_dt, nw_dt, la_dt;
+    int B, H;
+    int seq_len, cache_len;
+    int n_split, tps;
+    float qscale;  // sm_scale * log2(e): scores live in the base-2 domain
+    float eps;
+};
+
+template <int DT, int D>
+struct Geometry {
+    static constexpr int EPV = Vec<DT>::epv;  // elements per 16-byte vector
+    static constexpr int LPR = D / EPV;       // lanes per V row
+    static constexpr int TT = 64 * 8 / LPR;   // tokens per tile
+};
+
+__device__ __forceinline__ int current_len(const DecodeKArgs &a) {
+    return a.seq_len_dev ? min(*a.seq_len_dev, a.cache_len) : a.seq_len;
+}
+
+// GLA state update of one head; (1 - mix) * RMSNorm(y_I) * norm_w and mix go to the workspace.
+template <int DT, int D, int R>
+__device__ void state_block(const DecodeKArgs &a, int bh) {
+    using st = typename Stor<DT>::type;
+    constexpr int J = D - R;
+    constexpr int DV4 = D / 4;
+    constexpr int RG = kThreads / DV4;  // state rows per pass
+    constexpr int NPASS = (J + RG - 1) / RG;
+    __shared__ float s_v[D], s_k[J], s_q[J], s_g[J];
+    __shared__ float s_red[RG * D];
+    const int b = bh / a.H, h = bh % a.H;
+    const int tid = threadIdx.x;
+    const int d4 = (tid % DV4) * 4, jr = tid / DV4;
+    const float *sin = a.state_in + b * a.st_sb + h * a.st_sh;
+    f32x4 srow[NPASS];
+#pragma unroll
+    for (int i = 0; i < NPASS; ++i) {
+        const int j = jr + i * RG;
+        srow[i] = j < J ? *(const f32x4 *)(sin + j * D + d4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const st *qp = (const st *)a.q + b * a.q_sb + h * a.q_sh;
+    const st *kp = (const st *)a.k + b * a.k_sb + h * a.k_sh;
+    const st *vp = (const st *)a.v + b * a.v_sb + h * a.v_sh;
+    for (int i = tid; i < D; i += kThreads) s_v[i] = to_f32<DT>(vp[i * a.v_sd]);
+    const float lg = load_any(a.log_gamma, a.lg_dt, b * a.lg_sb + h * a.lg_sh);
+    for (int i = tid; i < J; i += kThreads) {
+        s_k[i] = to_f32<DT>(kp[(R + i) * a.k_sd]);
+        s_q[i] = to_f32<DT>(qp[(R + i) * a.q_sd]);
+        float e = lg;
+        if (a.log_alpha) e = lg * expf(load_any(a.log_alpha, a.la_dt, h * a.la_sh + i * a.la_sj));
+        s_g[i] = expf(e);
+    }
+    __syncthreads();
+    float *sout = a.state_out + b * a.so_sb + h * a.so_sh;
+    const f32x4 vv = {s_v[d4], s_v[d4 + 1], s_v[d4 + 2], s_v[d4 + 3]};
+    f32x4 yp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NPASS; ++i) {
+        const int j = jr + i * RG;
+        if (j < J) {
+            const f32x4 sn = s_g[j] * srow[i] + s_k[j] * vv;
+            *(f32x4 *)(sout + j * D + d4) = sn;
+            yp += s_q[j] * sn;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s_red[jr * D + d4 + c] = yp[c];
+    __syncthreads();
+    // Finish the inlier side: z = (1 - mix) * RMSNorm(y_I; eps) * norm_w.
+    float y = 0.f;
+    if (tid < D) {
+#pragma unroll
+        for (int r = 0; r < RG; ++r) y += s_red[r * D + tid];
+    }
+    float ss = wave_sum(y * y);  // D <= 128: waves 0 and 1 hold y
+    __shared__ float s_ss[kWaves];
+    if ((tid & 63) == 0) s_ss[tid >> 6] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) ss += s_ss[w];
+    const float mix = load_any(a.mix, a.mg_dt, b * a.mg_sb + h * a.mg_sh);
+    float *z = a.ws_z + bh * (D + 4);
+    if (tid < D) {
+        const float nw = load_any(a.norm_w, a.nw_dt, h * a.nw_sh + tid * a.nw_sd);
+        z[tid] = (1.f - mix) * (y * rsqrtf(ss / (float)D + a.eps) * nw);
+    }
+    if (tid == 0) z[D] = mix;
+}
+
+template <int DT, int D, int R>
+__global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeKArgs a) {
+    using st = typename Stor<DT>::type;
+    using G = Geometry<DT, D>;
+    constexpr int EPV = G::EPV, LPR = G::LPR, TT = G::TT;
+    constexpr int KL = R / EPV;          // lanes per K row
+    constexpr int NKL = TT * KL / 64;    // K vectors per lane per tile
+    constexpr int NVL = 8;               // V vectors per lane per tile
+    static_assert(KL >= 1 && KL <= LPR && (64 % KL) == 0 && NKL >= 1, "unsupported (D, R) geometry");
+    __shared__ float s_acc[kWaves][D];
+    __shared__ float s_ml[kWaves][2];
+
+    const int nbh = a.B * a.H;
+    if ((int)blockIdx.x < nbh) {
+        state_block<DT, D, R>(a, blockIdx.x);
+        return;
+    }
+    const int bh = (blockIdx.x - nbh) / a.n_split, split = (blockIdx.x - nbh) % a.n_split;
+    const int b = bh / a.H, h = bh % a.H;
+    const int seq_len = current_len(a);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int pk = lane % KL, pv = lane % LPR;
+    const int tpw = a.tps / kWaves;
+    const int ws = split * a.tps + wave * tpw;
+    const int we = min(ws + tpw, seq_len);
+
+    const st *qp = (const st *)a.q + b * a.q_sb + h * a.q_sh;
+    float qv[EPV];
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) qv[e] = to_f32<DT>(qp[(pk * EPV + e) * a.q_sd]) * a.qscale;
+
+    const st *ckh = (const st *)a.cache_k + b * a.ck_sb + h * a.ck_sh;
+    const st *cvh = (const st *)a.cache_v + b * a.cv_sb + h * a.cv_sh;
+    const int krow = (int)(a.ck_sl * sizeof(st)), vrow = (int)(a.cv_sl * sizeof(st));
+    const int nvalid = we > 0 ? we : 0;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void *)ckh, 0, nvalid * krow, kBufFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void *)cvh, 0, nvalid * vrow, kBufFlags);
+    const int koff0 = (lane / KL) * krow + pk * 16;
+    const int voff0 = (lane / LPR) * vrow + pv * 16;
+
+    float m_run = -INFINITY, l_run = 0.f;
+    float acc[EPV];
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) acc[e] = 0.f;
+
+    u32x4 kb[NKL], vb[NVL];
+    auto load_tile = [&](int t0, u32x4 *kd, u32x4 *vd) {
+#pragma unroll
+        for (int i = 0; i < NKL; ++i)
+            kd[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rk, koff0 + (t0 + 64 * i / KL) * krow, 0, kLoadNT));
+#pragma unroll
+        for (int i = 0; i < NVL; ++i)
+            vd[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rv, voff0 + (t0 + i * (64 / LPR)) * vrow, 0, kLoadNT));
+    };
+
+    if (ws < we) load_tile(ws, kb, vb);
+    for (int t0 = ws; t0 < we; t0 += TT) {
+        u32x4 kn[NKL], vn[NVL];
+        const bool more = t0 + TT < we;
+        if (more) load_tile(t0 + TT, kn, vn);
+
+        float s[NKL];
+#pragma unroll
+        for (int i = 0; i < NKL; ++i) {
+            float kf[EPV];
+            unpack16<DT>(kb[i], kf);
+            float acc_s = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) acc_s = fmaf(qv[e], kf[e], acc_s);
+#pragma unroll
+            for (int off = 1; off < KL; off <<= 1) acc_s += __shfl_xor(acc_s, off);
+            const int tok = t0 + (lane + 64 * i) / KL;
+            s[i] = tok < we ? acc_s : -INFINITY;
+        }
+        float mt = s[0];
+#pragma unroll
+        for (int i = 1; i < NKL; ++i) mt = fmaxf(mt, s[i]);
+        mt = wave_max(mt);
+        const float mn = fmaxf(m_run, mt);
+        const float sc = fast_exp2(m_run - mn);
+        float p[NKL];
+#pragma unroll
+        for (int i = 0; i < NKL; ++i) p[i] = fast_exp2(s[i] - mn);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) acc[e] *= sc;
+        float lsum = 0.f;
+#pragma unroll
+        for (int i = 0; i < NVL; ++i) {
+            // the score of V-token i lives in register (i*KL)/LPR of the lane heading its K row
+            const int src = ((lane / LPR + i * (64 / LPR)) * KL) & 63;
+            const float pi = __shfl(p[(i * KL) / LPR], src);
+            float vf[EPV];
+            unpack16<DT>(vb[i], vf);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pi, vf[e], acc[e]);
+            lsum += pi;
+        }
+        l_run = l_run * sc + lsum;
+        m_run = mn;
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < NKL; ++i) kb[i] = kn[i];
+#pragma unroll
+            for (int i = 0; i < NVL; ++i) vb[i] = vn[i];
+        }
+    }
+    // Lanes sharing pv hold disjoint token subsets of the same dims.
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1) {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) acc[e] += __shfl_xor(acc[e], off);
+        l_run += __shfl_xor(l_run, off);
+    }
+    if (lane < LPR) {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) s_acc[wave][lane * EPV + e] = acc[e];
+    }
+    if (lane == 0) {
+        s_ml[wave][0] = m_run;
+        s_ml[wave][1] = l_run;
+    }
+    __syncthreads();
+    // Merge the four waves; one partial per block.
+    float M = s_ml[0][0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_ml[w][0]);
+    float wgt[kWaves], L = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        wgt[w] = s_ml[w][0] == -INFINITY ? 0.f : fast_exp2(s_ml[w][0] - M);
+        L += wgt[w] * s_ml[w][1];
+    }
+    float *pacc = a.ws_acc + ((int64_t)bh * a.n_split + split) * D;
+    for (int d = threadIdx.x; d < D; d += kThreads) {
+        float o = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) o += wgt[w] * s_acc[w][d];
+        pacc[d] = o;
+    }
+    if (threadIdx.x == 0) *(float2 *)(a.ws_ml + ((int64_t)bh * a.n_split + split) * 2) = make_float2(M, L);
+}
+
+// One wave per head.  Every global load is issued before any of them is
+// consumed: lane p holds partial p's (max, denominator); the numerators of all
+// NS partials for the lane's dims sit in registers (indices past n_split are
+// clamped and weigh zero).
+template <int DT, int D, int NS>
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeKArgs a) {
+    using st = typename Stor<DT>::type;
+    constexpr int DPL = D / 64;  // dims per lane
+    const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
+    const int lane = threadIdx.x;
+    const int ns = a.n_split;
+    const float *pacc = a.ws_acc + (int64_t)bh * ns * D;
+    const float2 ml = lane < ns ? ((const float2 *)a.ws_ml)[(int64_t)bh * ns + lane] : make_float2(-INFINITY, 0.f);
+    float av[NS][DPL];
+#pragma unroll
+    for (int p = 0; p < NS; ++p) {
+        const int pc = min(p, ns - 1);
+#pragma unroll
+        for (int c = 0; c < DPL; ++c) av[p][c] = pacc[pc * D + lane + 64 * c];
+    }
+    const float *zp = a.ws_z + bh * (D + 4);
+    float z[DPL];
+#pragma unroll
+    for (int c = 0; c < DPL; ++c) z[c] = zp[lane + 64 * c];
+    const float mix = zp[D];
+
+    const float M = wave_max(ml.x);
+    const float w = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - M);
+    const float L = wave_sum(w * ml.y);
+    float ao[DPL];
+#pragma unroll
+    for (int c = 0; c < DPL; ++c) ao[c] = 0.f;
+#pragma unroll
+    for (int p = 0; p < NS; ++p) {
+        const float wp = p < ns ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), p)) : 0.f;
+#pragma unroll
+        for (int c = 0; c < DPL; ++c) ao[c] = fmaf(wp, av[p][c], ao[c]);
+    }
+    const float inv_l = 1.f / (L > 0.f ? L : 1.f);
+#pragma unroll
+    for (int c = 0; c < DPL; ++c)
+        ((st *)a.y)[b * a.y_sb + h * a.y_sh + (lane + 64 * c) * a.y_sd] = from_f32<DT>(fmaf(mix, ao[c] * inv_l, z[c]));
+}
+
+// ------------------------------------------------------------------ host
+int elem_size(int dt) { return dt == HOFA_F32 ? 4 : 2; }
+
+int tile_tokens(int dt, int D) { return 64 * 8 / (D * elem_size(dt) / 16); }
+
+int validate(const hofa_decode_args_t *a) {
+    HOFA_REQUIRE(a, HOFA_EINVAL, "hofa_decode: args is NULL");
+    HOFA_REQUIRE(a->B > 0 && a->H > 0, HOFA_EINVAL, "hofa_decode: B=%d H=%d must be positive", a->B, a->H);
+    HOFA_REQUIRE(a->D == 64 || a->D == 128, HOFA_EUNSUPPORTED, "hofa_decode: head dim D=%d not in {64,128}", a->D);
+    HOFA_REQUIRE((a->R == 16 || a->R == 32 || a->R == 64) && a->R < a->D && 8 * a->R >= a->D, HOFA_EUNSUPPORTED,
+                 "hofa_decode: outlier dims R=%d unsupported for D=%d (need R in {16,32,64}, R<D, 8R>=D)", a->R, a->D);
+    const int dt = a->q.dtype;
+    HOFA_REQUIRE(dt == HOFA_F32 || dt == HOFA_BF16 || dt == HOFA_F16, HOFA_EINVAL, "hofa_decode: bad dtype %d", dt);
+    HOFA_REQUIRE(a->k.dtype == dt && a->v.dtype == dt && a->cache_k.dtype == dt && a->cache_v.dtype == dt &&
+                     a->y.dtype == dt,
+                 HOFA_EINVAL, "hofa_decode: q, k, v, caches and y must share one dtype");
+    HOFA_REQUIRE(a->state_in.dtype == HOFA_F32 && a->state_out.dtype == HOFA_F32, HOFA_EINVAL,
+                 "hofa_decode: states must be float32");
+    HOFA_REQUIRE(a->q.data && a->k.data && a->v.data && a->cache_k.data && a->cache_v.data && a->state_in.data &&
+                     a->state_out.data && a->log_gamma.data && a->mix.data && a->norm_w.data && a->y.data,
+                 HOFA_EINVAL, "hofa_decode: NULL tensor pointer");
+    HOFA_REQUIRE(a->state_in.data != a->state_out.data, HOFA_EINVAL, "hofa_decode: state_out must not alias state_in");
+    const int J = a->D - a->R;
+    HOFA_REQUIRE(a->state_in.stride[3] == 1 && a->state_in.stride[2] == a->D && a->state_out.stride[3] == 1 &&
+                     a->state_out.stride[2] == a->D,
+                 HOFA_EINVAL, "hofa_decode: states must be contiguous [B,H,%d,%d]", J, a->D);
+    HOFA_REQUIRE(((uintptr_t)a->state_in.data % 16) == 0 && ((uintptr_t)a->state_out.data % 16) == 0 &&
+                     (a->state_in.stride[1] % 4) == 0 && (a->state_in.stride[0] % 4) == 0 &&
+                     (a->state_out.stride[1] % 4) == 0 && (a->state_out.stride[0] % 4) == 0,
+                 HOFA_EINVAL, "hofa_decode: states must be 16-byte aligned");
+    const int es = elem_size(dt);
+    HOFA_REQUIRE(a->cache_k.stride[3] == 1 && a->cache_v.stride[3] == 1, HOFA_EINVAL,
+                 "hofa_decode: caches must be contiguous in the last dim");
+    for (const hofa_view_t *c : {&a->cache_k, &a->cache_v}) {
+        HOFA_REQUIRE(((uintptr_t)c->data % 16) == 0 && (c->stride[0] * es) % 16 == 0 && (c->stride[1] * es) % 16 == 0 &&
+                         (c->stride[2] * es) % 16 == 0,
+                     HOFA_EINVAL, "hofa_decode: cache rows must be 16-byte aligned");
+    }
+    const int L = a->seq_len_dev ? a->cache_len : a->seq_len;
+    HOFA_REQUIRE(L >= 1, HOFA_EINVAL, "hofa_decode: seq_len=%d cache_len=%d must be >= 1", a->seq_len, a->cache_len);
+    HOFA_REQUIRE(a->seq_len_dev || a->cache_len <= 0 || a->seq_len <= a->cache_len, HOFA_EINVAL,
+                 "hofa_decode: seq_len=%d exceeds cache_len=%d", a->seq_len, a->cache_len);
+    HOFA_REQUIRE((int64_t)L * a->cache_v.stride[2] * es < (int64_t)1 << 31 &&
+                     (int64_t)L * a->cache_k.stride[2] * es < (int64_t)1 << 31,
+                 HOFA_EUNSUPPORTED, "hofa_decode: one head's cache must span less than 2 GiB");
+    HOFA_REQUIRE(a->split_k >= 0 && a->split_k <= kMaxSplit, HOFA_EINVAL, "hofa_decode: split_k=%d not in [0,%d]",
+                 a->split_k, kMaxSplit);
+    return HOFA_OK;
+}
+
+// Splits per head: about two stream blocks per CU, each wave at least two tiles.
+void plan(const hofa_decode_args_t *a, int *n_split, int *tps) {
+    const int unit = kWaves * tile_tokens(a->q.dtype, a->D);
+    const int L = a->seq_len_dev ? a->cache_len : a->seq_len;
+    int n;
+    if (a->split_k > 0) {
+        n = a->split_k;
+    } else {
+        const int bh = a->B * a->H;
+        const int target = (2 * device_cu_count() + bh - 1) / bh;
+        const int max_by_len = std::max(1, L / (2 * unit));
+        n = std::max(1, std::min(std::min(target, max_by_len), kMaxSplit));
+    }
+    int t = (L + n - 1) / n;
+    t = (t + unit - 1) / unit * unit;
+    *tps = t;
+    *n_split = (L + t - 1) / t;
+}
+
+size_t acc_bytes(const hofa_decode_args_t *a, int n_split) { return (size_t)a->B * a->H * n_split * a->D * 4; }
+
+size_t ml_bytes(const hofa_decode_args_t *a, int n_split) { return (size_t)a->B * a->H * n_split * 2 * 4; }
+
+size_t ws_bytes(const hofa_decode_args_t *a, int n_split) {
+    return acc_bytes(a, n_split) + ml_bytes(a, n_split) + (size_t)a->B * a->H * (a->D + 4) * 4;
+}
+
+template <int DT, int D, int R>
+void launch(const DecodeKArgs &k, hipStream_t s) {
+    const int bh = k.B * k.H;
+    hipLaunchKernelGGL((decode_stream_kernel<DT, D, R>), dim3(bh + bh * k.n_split), dim3(kThreads), 0, s, k);
+    if (k.n_split <= 8) hipLaunchKernelGGL((decode_merge_kernel<DT, D, 8>), dim3(bh), dim3(64), 0, s, k);
+    else if (k.n_split <= 16) hipLaunchKernelGGL((decode_merge_kernel<DT, D, 16>), dim3(bh), dim3(64), 0, s, k);
+    else if (k.n_split <= 32) hipLaunchKernelGGL((decode_merge_kernel<DT, D, 32>), dim3(bh), dim3(64), 0, s, k);
+    else hipLaunchKernelGGL((decode_merge_kernel<DT, D, 64>), dim3(bh), dim3(64), 0, s, k);
+}
+
+template <int DT>
+int dispatch(const DecodeKArgs &k, int D, int R, hipStream_t s) {
+    if (D == 64 && R == 16) launch<DT, 64, 16>(k, s);
+    else if (D == 64 && R == 32) launch<DT, 64, 32>(k, s);
+    else if (D == 128 && R == 16) launch<DT, 128, 16>(k, s);
+    else if (D == 128 && R == 32) launch<DT, 128, 32>(k, s);
+    else if (D == 128 && R == 64) launch<DT, 128, 64>(k, s);
+    else return HOFA_EUNSUPPORTED;
+    return HOFA_OK;
+}
+
+}  // namespace
+}  // namespace hofa
+
+using namespace hofa;
+
+extern "C" int hofa_decode_plan(const hofa_decode_args_t *a, int32_t *split_k, int32_t *tokens_per_split) {
+    int rc = validate(a);
+    if (rc) return rc;
+    int n, t;
+    plan(a, &n, &t);
+    if (split_k) *split_k = n;
+    if (tokens_per_split) *tokens_per_split = t;
+    return HOFA_OK;
+}
+
+extern "C" size_t hofa_decode_workspace_bytes(const hofa_decode_args_t *a) {
+    if (validate(a)) return 0;
+    int n, t;
+    plan(a, &n, &t);
+    return ws_bytes(a, n);
+}
+
+extern "C" int hofa_decode(const hofa_decode_args_t *a, void *workspace, size_t workspace_bytes, void *stream) {
+    int rc = validate(a);
+    if (rc) return rc;
+    int n, t;
+    plan(a, &n, &t);
+    const size_t need = ws_bytes(a, n);
+    HOFA_REQUIRE(workspace && workspace_bytes >= need, HOFA_EWORKSPACE,
+                 "hofa_decode: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
+    HOFA_REQUIRE(((uintptr_t)workspace % 16) == 0, HOFA_EWORKSPACE, "hofa_decode: workspace must be 16-byte aligned");
+
+    DecodeKArgs k{};
+    k.q = a->q.data; k.k = a->k.data; k.v = a->v.data;
+    k.cache_k = a->cache_k.data; k.cache_v = a->cache_v.data;
+    k.state_in = (const float *)a->state_in.data;
+    k.state_out = (float *)a->state_out.data;
+    k.log_gamma = a->log_gamma.data; k.mix = a->mix.data; k.norm_w = a->norm_w.data;
+    k.log_alpha = a->log_alpha.data;
+    k.y = (void *)a->y.data;
+    k.seq_len_dev = a->seq_len_dev;
+    k.ws_acc = (float *)workspace;
+    k.ws_ml = (float *)((char *)workspace + acc_bytes(a, n));
+    k.ws_z = (float *)((char *)workspace + acc_bytes(a, n) + ml_bytes(a, n));
+    k.q_sb = a->q.stride[0]; k.q_sh = a->q.stride[1]; k.q_sd = a->q.stride[3];
+    k.k_sb = a->k.stride[0]; k.k_sh = a->k.stride[1]; k.k_sd = a->k.stride[3];
+    k.v_sb = a->v.stride[0]; k.v_sh = a->v.stride[1]; k.v_sd = a->v.stride[3];
+    k.ck_sb = a->cache_k.stride[0]; k.ck_sh = a->cache_k.stride[1]; k.ck_sl = a->cache_k.stride[2];
+    k.cv_sb = a->cache_v.stride[0]; k.cv_sh = a->cache_v.stride[1]; k.cv_sl = a->cache_v.stride[2];
+    k.st_sb = a->state_in.stride[0]; k.st_sh = a->state_in.stride[1];
+    k.so_sb = a->state_out.stride[0]; k.so_sh = a->state_out.stride[1];
+    k.lg_sb = a->log_gamma.stride[0]; k.lg_sh = a->log_gamma.stride[1]; k.lg_dt = a->log_gamma.dtype;
+    k.mg_sb = a->mix.stride[0]; k.mg_sh = a->mix.stride[1]; k.mg_dt = a->mix.dtype;
+    k.nw_sh = a->norm_w.stride[0]; k.nw_sd = a->norm_w.stride[1]; k.nw_dt = a->norm_w.dtype;
+    k.la_sh = a->log_alpha.stride[0]; k.la_sj = a->log_alpha.stride[1]; k.la_dt = a->log_alpha.dtype;
+    k.y_sb = a->y.stride[0]; k.y_sh = a->y.stride[1]; k.y_sd = a->y.stride[3];
+    k.B = a->B; k.H = a->H;
+    k.seq_len = a->seq_len; k.cache_len = a->seq_len_dev ? a->cache_len : a->seq_len;
+    k.n_split = n; k.tps = t;
+    k.qscale = a->sm_scale * kLog2e;
+    k.eps = a->eps;
+
+    hipStream_t s = (hipStream_t)stream;
+    switch (a->q.dtype) {
+        case HOFA_F32: rc = dispatch<HOFA_F32>(k, a->D, a->R, s); break;
+        case HOFA_BF16: rc = dispatch<HOFA_BF16>(k, a->D, a->R, s); break;
+        default: rc = dispatch<HOFA_F16>(k, a->D, a->R, s); break;
+    }
+    if (rc) {
+        set_error("hofa_decode: no kernel for this (D, R)");
+        return rc;
+    }
+    return check_launch("hofa_decode");
+}

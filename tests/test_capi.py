@@ -1,0 +1,153 @@
+"""The C ABI library: it loads, exports every declared entry point, and its
+host-side argument checks reject bad calls before touching a GPU (CPU only)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from outlierneuronattention_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    src = open(os.path.join(ROOT, "include", "hofa.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(hofa_[a-z_0-9]+)\s*\(", src, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared_functions()
+    assert "hofa_decode" in names and len(names) >= 5
+    for n in names:
+        assert hasattr(lib, n), n
+    bound = {e[0] for e in _lib.EXPORTS}
+    assert set(names) == bound, set(names) ^ bound
+
+
+def test_version():
+    assert _lib.load().hofa_version() >= 1
+
+
+def _fake_view(dtype=_lib.HOFA_BF16, strides=(0, 0, 0, 1), addr=4096):
+    v = _lib.View()
+    v.data, v.dtype = addr, dtype
+    for i, s in enumerate(strides):
+        v.stride[i] = s
+    return v
+
+
+def _decode_args(B=1, H=2, D=64, R=16, L=256, dt=_lib.HOFA_BF16):
+    a = _lib.DecodeArgs()
+    a.B, a.H, a.D, a.R, a.seq_len, a.cache_len = B, H, D, R, L, L
+    a.sm_scale, a.eps = 2.0, 1e-7
+    J = D - R
+    a.q = a.k = a.v = a.y = _fake_view(dt, (H * D, D, D, 1))
+    a.cache_k = _fake_view(dt, (H * L * R, L * R, R, 1), 8192)
+    a.cache_v = _fake_view(dt, (H * L * D, L * D, D, 1), 16384)
+    a.state_in = _fake_view(_lib.HOFA_F32, (H * J * D, J * D, D, 1), 32768)
+    a.state_out = _fake_view(_lib.HOFA_F32, (H * J * D, J * D, D, 1), 65536)
+    a.log_gamma = a.mix = _fake_view(_lib.HOFA_F32, (H, 1, 0, 0))
+    a.norm_w = _fake_view(_lib.HOFA_F32, (D, 1, 0, 0))
+    return a
+
+
+def _expect_error(a, code, text):
+    lib = _lib.load()
+    rc = lib.hofa_decode(ctypes.byref(a), None, 0, None)
+    assert rc == code, (rc, lib.hofa_last_error())
+    assert text in lib.hofa_last_error().decode()
+    assert lib.hofa_decode_workspace_bytes(ctypes.byref(a)) == 0
+
+
+@pytest.mark.parametrize("field,value,code,text", [
+    ("D", 96, -2, "head dim"),
+    ("R", 8, -2, "outlier dims"),
+    ("R", 64, -2, "outlier dims"),
+    ("seq_len", 0, -1, "must be >= 1"),
+    ("split_k", 1000, -1, "split_k"),
+])
+def test_decode_rejects_bad_scalars(field, value, code, text):
+    a = _decode_args()
+    setattr(a, field, value)
+    _expect_error(a, code, text)
+
+
+def test_decode_rejects_layouts():
+    a = _decode_args()
+    a.cache_v = _fake_view(_lib.HOFA_BF16, (0, 0, 64, 2), 16384)
+    _expect_error(a, -1, "contiguous in the last dim")
+    a = _decode_args()
+    a.cache_k = _fake_view(_lib.HOFA_BF16, (0, 0, 12, 1), 8192)
+    _expect_error(a, -1, "16-byte aligned")
+    a = _decode_args()
+    a.state_out = a.state_in
+    _expect_error(a, -1, "alias")
+    a = _decode_args()
+    a.cache_v = _fake_view(_lib.HOFA_F16, (0, 0, 64, 1), 16384)
+    _expect_error(a, -1, "share one dtype")
+    a = _decode_args()
+    a.state_in = _fake_view(_lib.HOFA_BF16, (0, 0, 64, 1), 32768)
+    _expect_error(a, -1, "float32")
+
+
+def test_decode_workspace_needs_room():
+    lib = _lib.load()
+    a = _decode_args(L=4096)
+    n = lib.hofa_decode_workspace_bytes(ctypes.byref(a))
+    assert n > 0
+    rc = lib.hofa_decode(ctypes.byref(a), ctypes.c_void_p(1 << 20), n - 4, None)
+    assert rc == -4 and "workspace" in lib.hofa_last_error().decode()
+
+
+def test_python_wrapper_requires_gpu_tensors():
+    from outlierneuronattention_amd import fused_hofa_decode
+    q = torch.zeros(1, 2, 1, 64)
+    with pytest.raises(_lib.HofaError, match="GPU only"):
+        fused_hofa_decode(q, q, q, torch.zeros(1, 2, 8, 16), torch.zeros(1, 2, 8, 64), torch.zeros(1, 2, 48, 64),
+                          torch.zeros(1, 2, 48, 64), torch.zeros(1, 2, 1), torch.zeros(1, 2, 1), torch.ones(2, 64),
+                          16, 8, 2.0)
+    with pytest.raises(AssertionError):  # N == 1 check mirrors src/hofa_decode_triton.py:353
+        q2 = torch.zeros(1, 2, 2, 64)
+        fused_hofa_decode(q2, q2, q2, None, None, None, None, None, None, None, 16, 8, 2.0)
+
+
+def test_decode_wrapper_checks_extents_on_host():
+    """Extents never reach the C ABI (strides only), so the wrapper must refuse them."""
+    from outlierneuronattention_amd.hofa_decode import decode_args, log_alpha_strides
+    B, H, L, D, R = 2, 3, 64, 64, 16
+    J = D - R
+    q = torch.zeros(B, H, 1, D)
+    ck, cv = torch.zeros(B, H, L, R), torch.zeros(B, H, L, D)
+    s = torch.zeros(B, H, J, D)
+    lg, mix, nw = torch.zeros(B, H, 1), torch.zeros(B, H, 1), torch.ones(H, D)
+    a, y, _ = decode_args(q, q, q, ck, cv, s, s.clone(), lg, mix, nw, R, L, 2.0)
+    assert a.B == B and a.cache_len == L and y.shape == q.shape
+    bad = [
+        dict(cache_v=torch.zeros(B, H, L - 1, D)),
+        dict(cache_k=torch.zeros(B, H, L, 32)),
+        dict(state_I_in=torch.zeros(B, H, D, D)),
+        dict(norm_w=torch.ones(1, D)),
+        dict(log_gamma=torch.zeros(B, H + 1, 1)),
+        dict(mix_g=torch.zeros(B, H, 2)),
+        dict(seq_len=L + 1),
+        dict(seq_len=0),
+    ]
+    base = dict(q=q, k=q, v=q, cache_k=ck, cache_v=cv, state_I_in=s, state_I_out=s.clone(), log_gamma=lg,
+                mix_g=mix, norm_w=nw, R=R, seq_len=L, sm_scale=2.0)
+    for b in bad:
+        kw = dict(base, **b)
+        with pytest.raises(_lib.HofaError):
+            decode_args(**kw)
+    # log_alpha layouts: (h, j) strides and 1-D readings
+    la4 = torch.zeros(1, H, 1, J)
+    assert log_alpha_strides(la4, H, J)[1] == (J, 1)
+    assert log_alpha_strides(torch.zeros(H, J), H, J)[1] == (J, 1)
+    assert log_alpha_strides(torch.zeros(H * J), H, J)[1] == (J, 1)
+    assert log_alpha_strides(torch.zeros(J), H, J)[1] == (0, 1)
+    for shape in [(1, H, 1, J + 1), (H, J - 1), (H * J + 1,)]:
+        with pytest.raises(_lib.HofaError):
+            log_alpha_strides(torch.zeros(shape), H, J)
