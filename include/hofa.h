@@ -98,6 +98,87 @@ int hofa_decode_plan(const hofa_decode_args_t *args, int32_t *split_k, int32_t *
 
 int hofa_decode(const hofa_decode_args_t *args, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Outlier pathway of the prefill: causal softmax attention on the first R
+ * channels of Q/K against full-width V, mixed into the output.
+ *
+ * Replaces exact_attention_triton(q, k, v, r, sm_scale, mix_g, out, split_k)
+ * (src/exact_attention.py:163-188) and its kernel _fwd_kernel (:46-161):
+ *
+ *   O = softmax(Q[..., :R] K[..., :R]^T * sm_scale + causal mask) V
+ *   y = (accumulate ? y : 0) + mix * O        (mix = 1 when mix.data is NULL)
+ *
+ * Views (element strides b, h, t, d; q/k/v/y/o share one dtype f32|bf16|f16;
+ * the last stride must be 1 and rows 16-byte aligned):
+ *   q, k, v, y    [B,H,T,D]
+ *   mix           [B,H,T]   strides b, h, t (f32|bf16|f16)
+ *   o             optional [B,H,T,D]: O itself (data NULL = not written)
+ * lse (optional, float32 [B*H*T], NULL = not written) receives the base-2
+ * log-sum-exp of the scaled logits per query row (log2 of the softmax
+ * denominator, with logits multiplied by sm_scale*log2(e)).
+ * Supported: D in {64, 128}, R in {16, 32, 64}, R <= D.  bf16 and f32 use
+ * bf16 matrix cores (f32 logits from split hi/lo bf16 operands), f16 uses
+ * f16 matrix cores; accumulation is f32.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    int32_t B, H, T, D, R;
+    float sm_scale;
+    int32_t accumulate;
+    int32_t reserved;
+    hofa_view_t q, k, v;
+    hofa_view_t mix;
+    hofa_view_t y;
+    hofa_view_t o;
+    float *lse;
+} hofa_attn_fwd_args_t;
+
+int hofa_attn_fwd(const hofa_attn_fwd_args_t *args, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Inlier pathway of the prefill: chunked gated linear attention over the
+ * channels [R, D) of Q/K with full-width V, 64-token chunks.
+ *
+ * Replaces chunk_gla_inlier_fwd(Q, K, V, log_gamma, r, chunk_size, log_alpha,
+ * mix_g, gla_scale, out, states_in, requires_grad) (src/chunk_gla_inlier.py:153-237)
+ * and chunk_gla_fwd_kernel (:6-150):
+ *
+ *   S_t = diag(exp(g_t)) S_{t-1} + k_t^T v_t,   Y_I[t] = q_t S_t     (S_0 = 0)
+ *   g_{t,c} = log_gamma_t * exp(log_alpha[h, c])     (or the general g[t, c])
+ *   y = fuse_norm_gate ? (1 - mix) * gla_scale * RMSNorm(Y_I; eps) : Y_I
+ *   state_out = S_T
+ *
+ * Views (element strides; q/k/v/y share one dtype f32|bf16|f16, unit last
+ * stride, 16-byte aligned rows):
+ *   q, k, v, y     [B,H,T,D]      strides b, h, t, d
+ *   log_gamma      [B,H,T]        strides b, h, t (f32|bf16|f16); used when g.data is NULL
+ *   log_alpha      [H,J]          strides h, j; optional
+ *   g              [B,H,T,J] f32  strides b, h, t, j; optional general decay (wins over log_gamma)
+ *   mix            [B,H,T]        strides b, h, t (needed when fuse_norm_gate)
+ *   gla_scale      [H,D]          strides h, d (needed when fuse_norm_gate)
+ *   state_out      [B,H,J,D] f32  strides b, h, j, d
+ *   chunk_states   optional 16-bit [B*H][ceil(T/64)][2][D][J] receiving the
+ *                  state that enters each chunk, transposed, as a hi/lo pair
+ *                  of operands (hi + lo ~ the fp32 state), for a backward pass
+ * Supported: D in {64, 128}, J = D - R a multiple of 16.  Decay per token
+ * must be <= 0 (log of a factor in (0, 1]).  Matrix-core operands are split
+ * hi/lo 16-bit pairs, so the result tracks an fp32 computation.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    int32_t B, H, T, D, R;
+    float eps;
+    int32_t fuse_norm_gate;
+    int32_t reserved;
+    hofa_view_t q, k, v;
+    hofa_view_t log_gamma, log_alpha, g;
+    hofa_view_t mix, gla_scale;
+    hofa_view_t y;
+    hofa_view_t state_out;
+    void *chunk_states;
+} hofa_gla_fwd_args_t;
+
+size_t hofa_gla_fwd_workspace_bytes(const hofa_gla_fwd_args_t *args);
+int hofa_gla_fwd(const hofa_gla_fwd_args_t *args, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Library-wide helpers. */
 const char *hofa_last_error(void);
 int hofa_version(void);

@@ -43,12 +43,34 @@ class DecodeArgs(ctypes.Structure):
                 ("y", View)]
 
 
+class AttnFwdArgs(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("H", ctypes.c_int32), ("T", ctypes.c_int32), ("D", ctypes.c_int32),
+                ("R", ctypes.c_int32), ("sm_scale", ctypes.c_float), ("accumulate", ctypes.c_int32),
+                ("reserved", ctypes.c_int32),
+                ("q", View), ("k", View), ("v", View), ("mix", View), ("y", View), ("o", View),
+                ("lse", ctypes.c_void_p)]
+
+
+class GlaFwdArgs(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("H", ctypes.c_int32), ("T", ctypes.c_int32), ("D", ctypes.c_int32),
+                ("R", ctypes.c_int32), ("eps", ctypes.c_float), ("fuse_norm_gate", ctypes.c_int32),
+                ("reserved", ctypes.c_int32),
+                ("q", View), ("k", View), ("v", View),
+                ("log_gamma", View), ("log_alpha", View), ("g", View),
+                ("mix", View), ("gla_scale", View),
+                ("y", View), ("state_out", View),
+                ("chunk_states", ctypes.c_void_p)]
+
+
 # (name, restype, argtypes) of every entry point declared in include/hofa.h
 EXPORTS = [
     ("hofa_decode_workspace_bytes", ctypes.c_size_t, [ctypes.POINTER(DecodeArgs)]),
     ("hofa_decode_plan", ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_int32),
                                         ctypes.POINTER(ctypes.c_int32)]),
     ("hofa_decode", ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    ("hofa_attn_fwd", ctypes.c_int, [ctypes.POINTER(AttnFwdArgs), ctypes.c_void_p]),
+    ("hofa_gla_fwd_workspace_bytes", ctypes.c_size_t, [ctypes.POINTER(GlaFwdArgs)]),
+    ("hofa_gla_fwd", ctypes.c_int, [ctypes.POINTER(GlaFwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     ("hofa_last_error", ctypes.c_char_p, []),
     ("hofa_version", ctypes.c_int, []),
 ]
@@ -99,6 +121,37 @@ def view(t: torch.Tensor | None, strides=None) -> View:
     for i, s in enumerate(st[:4]):
         v.stride[i] = int(s)
     return v
+
+
+def expect_shape(t: torch.Tensor, shape, name: str) -> None:
+    if tuple(t.shape) != tuple(shape):
+        raise HofaError(f"{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+def per_token_strides(t: torch.Tensor, B: int, H: int, T: int, name: str):
+    """(b, h, t) strides of a per-(batch, head, token) scalar given as
+    ``[B|1, H|1, T]`` or ``[B|1, H|1, T, 1]`` (broadcast dims get stride 0)."""
+    if t.dim() == 4:
+        if t.shape[3] != 1:
+            raise HofaError(f"{name}: expected a trailing dim of 1, got {tuple(t.shape)}")
+    elif t.dim() != 3:
+        raise HofaError(f"{name}: expected [B,H,T] or [B,H,T,1], got {tuple(t.shape)}")
+    if t.shape[0] not in (1, B) or t.shape[1] not in (1, H) or t.shape[2] != T:
+        raise HofaError(f"{name}: expected [{B},{H},{T}], got {tuple(t.shape)}")
+    return tuple(t.stride(i) if t.shape[i] > 1 else 0 for i in range(3))
+
+
+def per_head_strides(t: torch.Tensor, H: int, W: int, name: str):
+    """(h, w) strides of a per-head row given as ``[1,H,1,W]``, ``[H,W]`` or
+    ``[H*W]`` (contiguous)."""
+    if t.dim() == 4 and t.shape[0] == 1 and t.shape[1] == H and t.shape[2] == 1 and t.shape[3] == W:
+        return t, (t.stride(1), t.stride(3))
+    if t.dim() == 2 and tuple(t.shape) == (H, W):
+        return t, (t.stride(0), t.stride(1))
+    if t.dim() == 1 and t.numel() == H * W:
+        t = t.contiguous()
+        return t, (W, 1)
+    raise HofaError(f"{name}: expected [1,{H},1,{W}], [{H},{W}] or [{H * W}], got {tuple(t.shape)}")
 
 
 def require_gpu(*tensors: torch.Tensor) -> None:

@@ -1,0 +1,142 @@
+// MFMA helpers for gfx950 (CDNA4), 64-wide waves.
+//
+// v_mfma_f32_32x32x16_{bf16,f16}: C[32x32] += A[32x16] * B[16x32]
+//   A operand, lane l: row l%32, k = 8*(l/32) + e  (e = 0..7, one 16-byte register quad)
+//   B operand, lane l: col l%32, k = 8*(l/32) + e
+//   C/D,       lane l: col l%32, rows 8*(v/4) + 4*(l/32) + v%4  (v = 0..15)
+// v_mfma_f32_16x16x32_{bf16,f16}: C[16x16] += A[16x32] * B[32x16]
+//   A operand, lane l: row l%16, k = 8*(l/16) + e
+//   B operand, lane l: col l%16, k = 8*(l/16) + e
+//   C/D,       lane l: col l%16, rows 4*(l/16) + v  (v = 0..3)
+// Both layouts were checked against a host matrix product on the device.
+#pragma once
+
+#include "hofa_common.h"
+
+namespace hofa {
+
+// 16-bit operand element type used with an input dtype: f16 inputs use the
+// f16 matrix cores, bf16 and f32 inputs use bf16 operands.
+template <int DT> constexpr bool kF16Ops = (DT == HOFA_F16);
+
+template <int DT>
+__device__ __forceinline__ f32x16 mfma32(const u32x4 &a, const u32x4 &b, const f32x16 &c) {
+    if constexpr (kF16Ops<DT>) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(const u32x4 &a, const u32x4 &b, const f32x4 &c) {
+    if constexpr (kF16Ops<DT>) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+    }
+}
+
+// Two floats -> one dword of 16-bit operands (lo in bits 0..15).
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    if constexpr (kF16Ops<DT>) {
+        return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+    } else {
+        return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ u32x4 pack8(const float *x) {
+    return u32x4{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3]), pack2<DT>(x[4], x[5]), pack2<DT>(x[6], x[7])};
+}
+
+// Eight consecutive entries x[off .. off+7] of an accumulator -> operand quad.
+template <int DT>
+__device__ __forceinline__ u32x4 pack8(const f32x16 &x, int off) {
+    return u32x4{pack2<DT>(x[off], x[off + 1]), pack2<DT>(x[off + 2], x[off + 3]), pack2<DT>(x[off + 4], x[off + 5]),
+                 pack2<DT>(x[off + 6], x[off + 7])};
+}
+
+// Split 8 floats into operand quads hi + lo with hi = round(x), lo = round(x - hi):
+// hi + lo carries about twice the operand mantissa into the matrix cores.
+template <int DT>
+__device__ __forceinline__ void split8(const float *x, u32x4 &hi, u32x4 &lo);
+
+template <int DT>
+__device__ __forceinline__ void split8v(const f32x16 &x, int off, u32x4 &hi, u32x4 &lo) {
+    float t[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = x[off + e];
+    split8<DT>(t, hi, lo);
+}
+
+// 16-bit operand -> float.
+template <int DT>
+__device__ __forceinline__ float op_to_f32(uint32_t bits16) {
+    if constexpr (kF16Ops<DT>) {
+        return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+    } else {
+        return __uint_as_float(bits16 << 16);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void split8(const float *x, u32x4 &hi, u32x4 &lo) {
+    hi = pack8<DT>(x);
+    float r[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        r[2 * e] = x[2 * e] - op_to_f32<DT>(hi[e] & 0xffffu);
+        r[2 * e + 1] = x[2 * e + 1] - op_to_f32<DT>(hi[e] >> 16);
+    }
+    lo = pack8<DT>(r);
+}
+
+// Load 8 consecutive input elements as one operand quad (converting f32 input).
+template <int DT>
+__device__ __forceinline__ u32x4 load_op8(const typename Stor<DT>::type *p) {
+    if constexpr (DT == HOFA_F32) {
+        const f32x4 a = *(const f32x4 *)p, b = *(const f32x4 *)(p + 4);
+        return u32x4{pack2<DT>(a[0], a[1]), pack2<DT>(a[2], a[3]), pack2<DT>(b[0], b[1]), pack2<DT>(b[2], b[3])};
+    } else {
+        return *(const u32x4 *)p;
+    }
+}
+
+// f32 input only: the bf16 rounding remainder of 8 consecutive elements
+// (x - bf16(x)), so hi + lo carries ~16 mantissa bits into the matrix cores.
+__device__ __forceinline__ u32x4 load_lo8_f32(const float *p) {
+    const f32x4 a = *(const f32x4 *)p, b = *(const f32x4 *)(p + 4);
+    float r[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        r[e] = a[e] - (float)(__bf16)a[e];
+        r[4 + e] = b[e] - (float)(__bf16)b[e];
+    }
+    return pack8<HOFA_BF16>(r);
+}
+
+// Block-index remap that keeps all blocks of one head on one XCD (blocks are
+// dispatched round-robin over 8 XCDs) and walks each head's row blocks from
+// the last to the first (longest causal rows first).
+__device__ __forceinline__ void xcd_remap(int blk, int nrow, int nhead, int *head, int *rowblk) {
+    constexpr int kXcd = 8;
+    if (nhead % kXcd == 0) {
+        const int xcd = blk % kXcd, slot = blk / kXcd;
+        *head = (slot / nrow) * kXcd + xcd;
+        *rowblk = nrow - 1 - slot % nrow;
+    } else {
+        *head = blk / nrow;
+        *rowblk = nrow - 1 - blk % nrow;
+    }
+}
+
+}  // namespace hofa
