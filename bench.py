@@ -136,6 +136,69 @@ def bench_decode_hot(B: int, steps: int):
     return dict(B=B, us_per_step=step_s * 1e6, gbs=decode_bytes(B) / step_s / 1e9)
 
 
+# ---------------------------------------------------------------- prefill (cfg2)
+P_B, P_T, P_H, P_D, P_R, P_C = 4, 4096, 16, 64, 16, 64
+P_J = P_D - P_R
+
+
+def prefill_flops(B=P_B, T=P_T, H=P_H, D=P_D, R=P_R) -> float:
+    """Algorithmic FLOPs of the attention core (causal, preprint Eq. 7):
+    B*H*T^2*(r + d_h) for the outlier softmax attention (QK^T and PV over the
+    causal half) plus 6*B*H*T*j*d_h for the chunked GLA."""
+    J = D - R
+    return B * H * T * T * (R + D) + 6 * B * H * T * J * D
+
+
+def make_prefill_inputs(gen, dev="cuda", B=P_B, T=P_T, H=P_H, D=P_D, R=P_R):
+    """cfg2: q/k/v ~ N(0,1) as [B,H,T,d] views of [B,T,H,3d] memory; per-channel
+    log decay clamp(logsigmoid(N(0,1))/16, -5, 0); mix = sigmoid(N(0,1)); gla_scale = 1."""
+    J = D - R
+    x = torch.randn(B, T, H, 3 * D, generator=gen).to(dev, torch.bfloat16)
+    q, k, v = (x[..., i * D:(i + 1) * D].transpose(1, 2) for i in range(3))
+    g = torch.clamp(F.logsigmoid(torch.randn(B, H, T, J, generator=gen)) / 16, -5, 0).to(dev)
+    mix = torch.sigmoid(torch.randn(B, H, T, generator=gen)).to(dev, torch.bfloat16)
+    gs = torch.ones(1, H, 1, D, device=dev)
+    lg = torch.zeros(B, H, T, device=dev)
+    return dict(q=q, k=k, v=v, g=g, mix=mix, gs=gs, lg=lg)
+
+
+def _prefill_call(inp, y):
+    from outlierneuronattention_amd.chunk_gla_inlier import chunk_gla_inlier_fwd
+    from outlierneuronattention_amd.exact_attention import exact_attention
+    chunk_gla_inlier_fwd(inp["q"], inp["k"], inp["v"], inp["lg"], P_R, P_C, mix_g=inp["mix"], gla_scale=inp["gs"],
+                         out=y, g=inp["g"])
+    exact_attention(inp["q"], inp["k"], inp["v"], P_R, math.sqrt(P_D / P_R), inp["mix"], out=y)
+
+
+def bench_prefill(steps: int, warmup: int):
+    gen = torch.Generator().manual_seed(4321)
+    inp = make_prefill_inputs(gen)
+    y = torch.empty(P_B, P_H, P_T, P_D, dtype=torch.bfloat16, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(max(2, warmup)):
+            _prefill_call(inp, y)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            _prefill_call(inp, y)
+        g.replay()
+        s.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(s)
+        for _ in range(steps):
+            g.replay()
+        t1.record(s)
+        torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    fl = prefill_flops()
+    tfs = fl / (ms * 1e-3) / 1e12
+    return dict(workload="cfg2: chunked prefill forward, B=4 T=4096 H=16 d_h=64 r=16 (j=48), GLA chunk 64, bf16",
+                ms_per_call=round(ms, 4), gflop=round(fl / 1e9, 2), tflops=round(tfs, 1),
+                mfma_frac=round(tfs / MFMA_BF16_PEAK_TFS, 4))
+
+
 def cpu_baseline_decode(B: int, budget_s: float = 10.0):
     """Oracle decode step (torch CPU fp32) on the cfg3 shape: time until the
     budget is spent (at least 2 steps after one warm-up)."""
@@ -199,6 +262,7 @@ def main():
     head = bench_decode(args.batch, args.steps, args.warmup)
     side = bench_decode(other, args.steps, args.warmup)
     hot = bench_decode_hot(1, min(args.steps, 500))
+    prefill = bench_prefill(max(5, min(50, args.steps // 20)), 3)
     cpu = None if args.skip_cpu else cpu_baseline_decode(args.batch, args.cpu_budget)
     achieved = head["gbs"]
     line = {
@@ -225,6 +289,7 @@ def main():
         "decode": {f"B{head['B']}": {k: round(v, 4) if isinstance(v, float) else v for k, v in head.items()},
                    f"B{side['B']}": {k: round(v, 4) if isinstance(v, float) else v for k, v in side.items()},
                    "B1_llc_resident": {k: round(v, 3) if isinstance(v, float) else v for k, v in hot.items()}},
+        "prefill_fwd": prefill,
     }
     print(json.dumps(line), flush=True)
 
