@@ -199,6 +199,80 @@ def bench_prefill(steps: int, warmup: int):
                 mfma_frac=round(tfs / MFMA_BF16_PEAK_TFS, 4))
 
 
+# ---------------------------------------------------------------- training (cfg4)
+T_B, T_T, T_H, T_D, T_R = 8, 2048, 12, 64, 16
+
+
+def train_flops(B=T_B, T=T_T, H=T_H, D=T_D, R=T_R):
+    """Algorithmic FLOPs of the attention core, forward and backward (causal):
+    forward B*H*T^2*(r + d_h) + 6*B*H*T*j*d_h; backward B*H*T^2*(3r + 2d_h)
+    (QK^T recompute, dO V^T, dV, dK, dQ) + 12*B*H*T*j*d_h."""
+    J = D - R
+    fwd = B * H * T * T * (R + D) + 6 * B * H * T * J * D
+    bwd = B * H * T * T * (3 * R + 2 * D) + 12 * B * H * T * J * D
+    return fwd, bwd
+
+
+def make_train_inputs(gen, dev="cuda"):
+    """cfg4 at kernel level: bf16 q/k/v ~ N(0,1) ([B,H,T,d] views of [B,T,H,3d]),
+    learnable per-(head, channel) decay: log_gamma = -1 and log_alpha =
+    log(-logsigmoid(U(2,6))), so g[t, c] = logsigmoid(U(2,6))[c]; mix =
+    sigmoid(N(0,1)); gla_scale = 1; dO ~ N(0,1).  Decay and gate parameters fp32."""
+    B, T, H, D, R = T_B, T_T, T_H, T_D, T_R
+    J = D - R
+    x = torch.randn(B, T, H, 3 * D, generator=gen).to(dev, torch.bfloat16)
+    q, k, v = (x[..., i * D:(i + 1) * D].transpose(1, 2) for i in range(3))
+    q_o = q[..., :R]
+    k_o = k[..., :R]
+    lg = torch.full((B, H, T), -1.0, device=dev)
+    la = torch.log(-F.logsigmoid(2 + 4 * torch.rand(1, H, 1, J, generator=gen))).to(dev)
+    mix = torch.sigmoid(torch.randn(B, H, T, generator=gen)).to(dev)
+    gs = torch.ones(1, H, 1, D, device=dev)
+    dy = torch.randn(B, H, T, D, generator=gen).to(dev, torch.bfloat16)
+    leaves = dict(q=q.detach(), k=k.detach(), v=v.detach(), lg=lg, la=la, mix=mix, gs=gs)
+    for t in leaves.values():
+        t.requires_grad_()
+    return leaves, dy
+
+
+def _train_step(inp, dy, backward=True):
+    from outlierneuronattention_amd.autograd import hofa_core
+    q, k = inp["q"], inp["k"]
+    y = hofa_core(q[..., :T_R], k[..., :T_R], q, k, inp["v"], inp["lg"], inp["la"], inp["mix"], inp["gs"], T_R,
+                  math.sqrt(T_D / T_R))
+    if backward:
+        y.backward(dy)
+    return y
+
+
+def bench_train(steps: int, warmup: int):
+    gen = torch.Generator().manual_seed(777)
+    inp, dy = make_train_inputs(gen)
+    for _ in range(max(2, warmup)):
+        _train_step(inp, dy)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ev[0].record(s)
+    for _ in range(steps):
+        _train_step(inp, dy)
+    ev[1].record(s)
+    with torch.no_grad():
+        for _ in range(steps):
+            _train_step(inp, dy, backward=False)
+    ev[2].record(s)
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / steps
+    ms_fwd = ev[1].elapsed_time(ev[2]) / steps
+    fwd, bwd = train_flops()
+    tfs = (fwd + bwd) / (ms * 1e-3) / 1e12
+    return dict(workload="cfg4: attention core fwd+bwd, B=8 T=2048 H=12 d_h=64 r=16 (j=48), learnable "
+                         "per-channel decay, bf16 operands, fp32 decay/gate grads (projections excluded)",
+                ms_per_step=round(ms, 4), ms_fwd_only=round(ms_fwd, 4), gflop=round((fwd + bwd) / 1e9, 2),
+                tflops=round(tfs, 1), mfma_frac=round(tfs / MFMA_BF16_PEAK_TFS, 4),
+                timing="eager launches (autograd), HIP events on the current stream")
+
+
 def cpu_baseline_decode(B: int, budget_s: float = 10.0):
     """Oracle decode step (torch CPU fp32) on the cfg3 shape: time until the
     budget is spent (at least 2 steps after one warm-up)."""
@@ -263,6 +337,7 @@ def main():
     side = bench_decode(other, args.steps, args.warmup)
     hot = bench_decode_hot(1, min(args.steps, 500))
     prefill = bench_prefill(max(5, min(50, args.steps // 20)), 3)
+    train = bench_train(max(5, min(20, args.steps // 50)), 3)
     cpu = None if args.skip_cpu else cpu_baseline_decode(args.batch, args.cpu_budget)
     achieved = head["gbs"]
     line = {
@@ -290,6 +365,7 @@ def main():
                    f"B{side['B']}": {k: round(v, 4) if isinstance(v, float) else v for k, v in side.items()},
                    "B1_llc_resident": {k: round(v, 3) if isinstance(v, float) else v for k, v in hot.items()}},
         "prefill_fwd": prefill,
+        "train_fwd_bwd": train,
     }
     print(json.dumps(line), flush=True)
 

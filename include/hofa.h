@@ -156,12 +156,18 @@ int hofa_attn_fwd(const hofa_attn_fwd_args_t *args, void *stream);
  *   mix            [B,H,T]        strides b, h, t (needed when fuse_norm_gate)
  *   gla_scale      [H,D]          strides h, d (needed when fuse_norm_gate)
  *   state_out      [B,H,J,D] f32  strides b, h, j, d
- *   chunk_states   optional 16-bit [B*H][ceil(T/64)][2][D][J] receiving the
- *                  state that enters each chunk, transposed, as a hi/lo pair
- *                  of operands (hi + lo ~ the fp32 state), for a backward pass
+ *   chunk_states   optional 16-bit [B*H][ceil(T/64)][4][D*J] receiving the
+ *                  state that enters each chunk as bf16 hi/lo operand pairs
+ *                  (hi + lo ~ the fp32 state): planes 0/1 transposed [D][J],
+ *                  planes 2/3 as [J][D]; saved for hofa_gla_bwd
+ *   n_out          optional [B,H,T,D] (dtype of y): RMSNorm(Y_I) before the
+ *                  gate, saved for hofa_gla_bwd (needs fuse_norm_gate)
+ *   rstd           float32 [B*H*T] receiving 1/sqrt(mean(Y_I^2) + eps) when
+ *                  n_out is given
  * Supported: D in {64, 128}, J = D - R a multiple of 16.  Decay per token
  * must be <= 0 (log of a factor in (0, 1]).  Matrix-core operands are split
- * hi/lo 16-bit pairs, so the result tracks an fp32 computation.
+ * hi/lo bf16 pairs for every input dtype, so the result tracks an fp32
+ * computation.
  * ---------------------------------------------------------------------- */
 typedef struct {
     int32_t B, H, T, D, R;
@@ -174,10 +180,85 @@ typedef struct {
     hofa_view_t y;
     hofa_view_t state_out;
     void *chunk_states;
+    hofa_view_t n_out;
+    float *rstd;
 } hofa_gla_fwd_args_t;
 
 size_t hofa_gla_fwd_workspace_bytes(const hofa_gla_fwd_args_t *args);
 int hofa_gla_fwd(const hofa_gla_fwd_args_t *args, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Backward of the outlier pathway (causal softmax attention, QK width R,
+ * value width D).
+ *
+ * No reference kernel: the reference trains through autograd of torch SDPA
+ * (src/HybridOutlierFactorizedAttentionTrain.py:258-259).  Given the
+ * upstream gradient dout of O = softmax(Q K^T sm_scale) V, the base-2 lse
+ * written by hofa_attn_fwd and delta = rowsum(dout (.) O):
+ *   dv = P^T dout (+ dv when dv_accumulate), dq = sm_scale dS K,
+ *   dk = sm_scale dS^T Q,  dS = P (.) (dout V^T - delta)
+ * Views (element strides b, h, t, d; one dtype f32|bf16|f16; unit last
+ * stride, 16-byte aligned rows): q, k, dq, dk [B,H,T,>=R] (columns [0,R)
+ * used / written); v, dout, dv [B,H,T,D].  lse, delta float32 [B*H*T].
+ * Supported: D in {64, 128}, R in {16, 32, 64}, R <= D.  Matrix-core
+ * operands are 16-bit (bf16 for bf16/f32 inputs, f16 for f16), f32 accumulate.
+ * Two kernels (dk/dv per key block, dq per query block), no atomics.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    int32_t B, H, T, D, R;
+    float sm_scale;
+    int32_t dv_accumulate;
+    int32_t reserved;
+    hofa_view_t q, k, v, dout;
+    const float *lse;
+    const float *delta;
+    hofa_view_t dq, dk, dv;
+} hofa_attn_bwd_args_t;
+
+int hofa_attn_bwd(const hofa_attn_bwd_args_t *args, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Backward of the inlier pathway and of the fused norm/gate epilogue.
+ *
+ * No reference kernel: the reference trains through autograd of fla's
+ * chunk_gla, nn.RMSNorm, the gla_scale product and torch.lerp
+ * (src/HybridOutlierFactorizedAttentionTrain.py:263-294).  For
+ *   Y = (1 - mix) * gla_scale * N + mix * O,   N = RMSNorm(Y_I; eps),
+ *   Y_I = GLA(q[..., R:], k[..., R:], v, g)
+ * and the upstream gradient dy, writes
+ *   dq, dk          columns [R, D) (columns [0, R) are not touched)
+ *   dv              the GLA part of dv (overwritten)
+ *   d_log_gamma     [B,H,T] (scalar decay) or d_g [B,H,T,J] f32 (general g)
+ *   d_log_alpha     [H,J] (when log_alpha is given; optional)
+ *   d_mix           [B,H,T] (optional; mix.data NULL means mix = 0)
+ *   d_gla_scale     [H,D]
+ *   dout_attn       optional [B,H,T,D] = mix * dy, and delta float32 [B*H*T]
+ *                   = rowsum(dout_attn (.) O): the inputs of hofa_attn_bwd
+ * Saved from the forward: n = RMSNorm(Y_I) and rstd (hofa_gla_fwd n_out /
+ * rstd), chunk_states (four planes), o = the attention output O
+ * (hofa_attn_fwd o; needed for d_mix and delta).
+ * Views as in hofa_gla_fwd; dq, dk, dv, dy, n, o, dout_attn share the dtype
+ * of q.  Small per-head / per-token outputs take any dtype.  Matrix-core
+ * operands are hi/lo bf16 pairs (fp32-like products), like the forward.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    int32_t B, H, T, D, R;
+    int32_t reserved;
+    hofa_view_t q, k, v;
+    hofa_view_t log_gamma, log_alpha, g;
+    hofa_view_t mix, gla_scale;
+    hofa_view_t n, o;
+    const float *rstd;
+    const void *chunk_states;
+    hofa_view_t dy;
+    hofa_view_t dq, dk, dv;
+    hofa_view_t d_log_gamma, d_g, d_log_alpha, d_mix, d_gla_scale;
+    hofa_view_t dout_attn;
+    float *delta;
+} hofa_gla_bwd_args_t;
+
+size_t hofa_gla_bwd_workspace_bytes(const hofa_gla_bwd_args_t *args);
+int hofa_gla_bwd(const hofa_gla_bwd_args_t *args, void *workspace, size_t workspace_bytes, void *stream);
 
 /* Library-wide helpers. */
 const char *hofa_last_error(void);

@@ -59,7 +59,32 @@ class GlaFwdArgs(ctypes.Structure):
                 ("log_gamma", View), ("log_alpha", View), ("g", View),
                 ("mix", View), ("gla_scale", View),
                 ("y", View), ("state_out", View),
-                ("chunk_states", ctypes.c_void_p)]
+                ("chunk_states", ctypes.c_void_p),
+                ("n_out", View), ("rstd", ctypes.c_void_p)]
+
+
+class AttnBwdArgs(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("H", ctypes.c_int32), ("T", ctypes.c_int32), ("D", ctypes.c_int32),
+                ("R", ctypes.c_int32), ("sm_scale", ctypes.c_float), ("dv_accumulate", ctypes.c_int32),
+                ("reserved", ctypes.c_int32),
+                ("q", View), ("k", View), ("v", View), ("dout", View),
+                ("lse", ctypes.c_void_p), ("delta", ctypes.c_void_p),
+                ("dq", View), ("dk", View), ("dv", View)]
+
+
+class GlaBwdArgs(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("H", ctypes.c_int32), ("T", ctypes.c_int32), ("D", ctypes.c_int32),
+                ("R", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("q", View), ("k", View), ("v", View),
+                ("log_gamma", View), ("log_alpha", View), ("g", View),
+                ("mix", View), ("gla_scale", View),
+                ("n", View), ("o", View),
+                ("rstd", ctypes.c_void_p), ("chunk_states", ctypes.c_void_p),
+                ("dy", View),
+                ("dq", View), ("dk", View), ("dv", View),
+                ("d_log_gamma", View), ("d_g", View), ("d_log_alpha", View), ("d_mix", View),
+                ("d_gla_scale", View),
+                ("dout_attn", View), ("delta", ctypes.c_void_p)]
 
 
 # (name, restype, argtypes) of every entry point declared in include/hofa.h
@@ -71,6 +96,9 @@ EXPORTS = [
     ("hofa_attn_fwd", ctypes.c_int, [ctypes.POINTER(AttnFwdArgs), ctypes.c_void_p]),
     ("hofa_gla_fwd_workspace_bytes", ctypes.c_size_t, [ctypes.POINTER(GlaFwdArgs)]),
     ("hofa_gla_fwd", ctypes.c_int, [ctypes.POINTER(GlaFwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    ("hofa_attn_bwd", ctypes.c_int, [ctypes.POINTER(AttnBwdArgs), ctypes.c_void_p]),
+    ("hofa_gla_bwd_workspace_bytes", ctypes.c_size_t, [ctypes.POINTER(GlaBwdArgs)]),
+    ("hofa_gla_bwd", ctypes.c_int, [ctypes.POINTER(GlaBwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     ("hofa_last_error", ctypes.c_char_p, []),
     ("hofa_version", ctypes.c_int, []),
 ]

@@ -13,37 +13,91 @@ forward after projections, gates and RoPE (SDPA + fla ``chunk_gla`` +
 ``q_o``/``k_o`` are the RoPE'd outlier channels, ``q``/``k`` the projections
 whose channels ``[r, d_head)`` feed the GLA.  With ``r == 0`` (and no mix) it
 is the pure-GLA branch ``gla_scale * RMSNorm(GLA)`` (:201-223).
+
+The backward runs the HIP kernel pair ``hofa_gla_bwd`` (epilogue + inlier
+GLA) then ``hofa_attn_bwd`` (outlier softmax attention, accumulating into
+dv); the reference relies on autograd through SDPA and fla instead.
 """
 from __future__ import annotations
 
 import torch
 
-from .chunk_gla_inlier import chunk_gla_inlier_fwd
-from .exact_attention import exact_attention
+from .chunk_gla_inlier import chunk_gla_inlier_bwd, chunk_gla_inlier_fwd, chunk_states_numel
+from .exact_attention import exact_attention, exact_attention_bwd
 
 FP32_EPS = float(torch.finfo(torch.float32).eps)
+
+
+def _rows_ok(t: torch.Tensor) -> torch.Tensor:
+    """The kernels need unit last stride and 16-byte aligned rows."""
+    es = t.element_size()
+    if t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((s * es) % 16 == 0 for s in t.stride()[:-1]):
+        return t
+    return t.contiguous()
+
+
+def _grad_like(g: torch.Tensor, ref: torch.Tensor) -> torch.Tensor:
+    """Reduce a full-shape gradient to a broadcast input's shape and dtype."""
+    if tuple(g.shape) != tuple(ref.shape):
+        g = g.sum_to_size(ref.shape) if g.numel() != ref.numel() else g.reshape(ref.shape)
+    return g.to(ref.dtype)
 
 
 class _HOFACore(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q_o, k_o, q, k, v, log_gamma, log_alpha, mix, gla_scale, r, sm_scale):
         B, H, T, D = v.shape
-        if mix is None:  # pure GLA: Y = gla_scale * RMSNorm(GLA)
-            mix_eff = torch.zeros(B, H, T, dtype=v.dtype, device=v.device)
-        else:
-            mix_eff = mix
-        y = torch.empty(B, H, T, D, dtype=v.dtype, device=v.device)
+        J = D - r
+        dev = v.device
+        train = any(ctx.needs_input_grad[:9])
+        mix_eff = torch.zeros(B, H, T, dtype=v.dtype, device=dev) if mix is None else mix
+        y = torch.empty(B, H, T, D, dtype=v.dtype, device=dev)
+        n = rstd = cs = o = lse = None
+        if train:
+            n = torch.empty(B, H, T, D, dtype=v.dtype, device=dev)
+            rstd = torch.empty(B * H * T, dtype=torch.float32, device=dev)
+            cs = torch.empty(chunk_states_numel(B, H, T, D, J), dtype=torch.int16, device=dev)
         chunk_gla_inlier_fwd(q, k, v, log_gamma, r, 64, log_alpha=log_alpha, mix_g=mix_eff, gla_scale=gla_scale,
-                             out=y, eps=FP32_EPS)
+                             out=y, eps=FP32_EPS, chunk_states=cs, n_out=n, rstd=rstd)
         if r > 0:
-            exact_attention(q_o, k_o, v, r, sm_scale, mix_eff, out=y)
-        ctx.mark_non_differentiable()
+            if train and mix is not None:
+                o = torch.empty(B, H, T, D, dtype=v.dtype, device=dev)
+                lse = torch.empty(B * H * T, dtype=torch.float32, device=dev)
+            exact_attention(q_o, k_o, v, r, sm_scale, mix_eff, out=y, o=o, lse=lse)
+        if train:
+            ctx.save_for_backward(q_o, k_o, q, k, v, log_gamma, log_alpha, mix, gla_scale, n, rstd, cs, o, lse)
+            ctx.r, ctx.sm_scale = r, sm_scale
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        raise NotImplementedError("the backward kernels of the HOFA core are not available in this build")
+        q_o, k_o, q, k, v, log_gamma, log_alpha, mix, gla_scale, n, rstd, cs, o, lse = ctx.saved_tensors
+        r, sm_scale = ctx.r, ctx.sm_scale
+        dy = _rows_ok(dy.to(v.dtype))
+        attn = r > 0 and mix is not None
+        g = chunk_gla_inlier_bwd(q, k, v, log_gamma, r, dy, n, rstd, cs, gla_scale, log_alpha=log_alpha, mix_g=mix,
+                                 o=o, want_attn_grad=attn)
+        dq, dk, dv = g["dq"], g["dk"], g["dv"]
+        if r > 0:
+            dq[..., :r].zero_()
+            dk[..., :r].zero_()
+        dq_o = dk_o = None
+        if attn:
+            dq_o, dk_o, _ = exact_attention_bwd(q_o, k_o, v, g["dout_attn"], lse, g["delta"], r, sm_scale,
+                                                dv=dv, dv_accumulate=True)
+        elif r > 0:
+            dq_o, dk_o = torch.zeros_like(q_o), torch.zeros_like(k_o)
+        d_lg = _grad_like(g["d_log_gamma"], log_gamma)
+        d_la = _grad_like(g["d_log_alpha"], log_alpha) if log_alpha is not None else None
+        d_mix = _grad_like(g["d_mix"], mix) if mix is not None else None
+        d_gs = _grad_like(g["d_gla_scale"], gla_scale)
+        if dq_o is not None:
+            dq_o, dk_o = dq_o.to(q_o.dtype), dk_o.to(k_o.dtype)
+        return dq_o, dk_o, dq, dk, dv, d_lg, d_la, d_mix, d_gs, None, None
 
 
 def hofa_core(q_o, k_o, q, k, v, log_gamma, log_alpha, mix, gla_scale, r: int, sm_scale: float):
+    q, k, v = _rows_ok(q), _rows_ok(k), _rows_ok(v)
+    if q_o is not None:
+        q_o, k_o = _rows_ok(q_o), _rows_ok(k_o)
     return _HOFACore.apply(q_o, k_o, q, k, v, log_gamma, log_alpha, mix, gla_scale, int(r), float(sm_scale))

@@ -99,6 +99,17 @@ __device__ __forceinline__ float load_any(const void *p, int dtype, int64_t idx)
     return (float)__builtin_bit_cast(_Float16, b);
 }
 
+// Scalar store with the element type chosen at run time (round to nearest even).
+__device__ __forceinline__ void store_any(void *p, int dtype, int64_t idx, float x) {
+    if (dtype == HOFA_F32) {
+        ((float *)p)[idx] = x;
+    } else if (dtype == HOFA_BF16) {
+        ((uint16_t *)p)[idx] = __builtin_bit_cast(uint16_t, (__bf16)x);
+    } else {
+        ((uint16_t *)p)[idx] = __builtin_bit_cast(uint16_t, (_Float16)x);
+    }
+}
+
 // ---------------------------------------------------------------- wave ops
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll

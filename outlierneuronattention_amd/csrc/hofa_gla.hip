@@ -11,8 +11,8 @@
 //        dS^T[D x J] = V_c^T (K_c (.) exp(G_last - G))        v_mfma_f32_16x16x32
 //      every exponent <= 0.  Writes dS^T and G_last.
 //   2. gla_scan_kernel    grid (B*H, D*J/1024): S_in(c) = S, S <- exp(G_last) S + dS,
-//      writes S_in(c) transposed as a hi/lo pair of 16-bit operands and the
-//      final fp32 state.
+//      writes S_in(c) transposed as a hi/lo pair of 16-bit operands (and, for
+//      a backward pass, untransposed as a second pair) and the final fp32 state.
 //   3. gla_out_kernel     grid (B*H*nc), 2 waves x 32 query rows:
 //        A^T[key, query] = K~ Q~^T     K~ = K (.) exp(-G), Q~ = Q (.) exp(G)   (masked key <= query)
 //        Y^T[dv, query]  = V_c^T A^T + S_in^T Q~^T                           v_mfma_f32_32x32x16
@@ -21,153 +21,17 @@
 //      reduces over D inside a lane pair.  K~ grows like exp(-G); a chunk
 //      whose decay range exceeds kSafeRange computes A^T element-wise with
 //      differences G_q - G_k <= 0 instead.
-// Every matrix-core product takes its operands as hi + lo pairs of 16-bit
-// values (x ~ hi + lo, see split8), i.e. about 16 mantissa bits: the result
-// tracks an fp32 computation rather than one rounded to bf16 operands.
-#include "hofa_mfma.h"
+// Every matrix-core product takes its operands as hi + lo pairs of bf16
+// values (x ~ hi + lo, see split8), i.e. about 16 mantissa bits in the f32
+// exponent range: the result tracks an fp32 computation rather than one
+// rounded to 16-bit operands (f16 inputs use the same bf16 pairs).
+#include "hofa_gla_common.h"
 
 namespace hofa {
 namespace {
 
-constexpr int C = 64;             // chunk length
-constexpr int NT = 128;           // threads of the chunk kernels
-constexpr float kSafeRange = 64.f;  // max in-chunk -G for the factored form (exp(64) ~ 6e27)
-
-struct GlaK {
-    const void *q, *k, *v, *lg, *la, *g, *mix, *gs;
-    void *y;
-    float *state_out;
-    float *ws_ds;       // [B*H][nc][D][J] f32
-    float *ws_gl;       // [B*H][nc][J] f32
-    uint16_t *s_in;     // [B*H][nc][2][D][J] entering states: hi then lo 16-bit operands
-    int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, y_sb, y_sh, y_st;
-    int64_t lg_sb, lg_sh, lg_st, la_sh, la_sj, g_sb, g_sh, g_st, g_sj;
-    int64_t m_sb, m_sh, m_st, gs_sh, gs_sd;
-    int64_t so_sb, so_sh, so_sj, so_sd;
-    int lg_dt, la_dt, mix_dt, gs_dt;
-    int B, H, T, R, nc;
-    int fuse;
-    float eps;
-};
-
-// In-chunk inclusive cumsum of the log decay into sG[C][J] (tokens past T decay by 0).
-template <int J, bool GENERAL>
-__device__ void chunk_cumsum(const GlaK &a, int b, int h, int t0, float *sG, float *sAux) {
-    const int tid = threadIdx.x;
-    if constexpr (!GENERAL) {
-        float *sLam = sAux, *sAl = sAux + C;
-        if (tid < 64) {
-            const int t = t0 + tid;
-            float x = t < a.T ? load_any(a.lg, a.lg_dt, b * a.lg_sb + h * a.lg_sh + (int64_t)t * a.lg_st) : 0.f;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float y = __shfl_up(x, off);
-                if (tid >= off) x += y;
-            }
-            sLam[tid] = x;
-        }
-        for (int c = tid; c < J; c += NT) sAl[c] = a.la ? expf(load_any(a.la, a.la_dt, h * a.la_sh + c * a.la_sj)) : 1.f;
-        __syncthreads();
-        for (int idx = tid; idx < C * J; idx += NT) sG[idx] = sLam[idx / J] * sAl[idx % J];
-    } else {
-        const float *gp = (const float *)a.g + b * a.g_sb + h * a.g_sh;
-        for (int c = tid; c < J; c += NT) {
-            float acc = 0.f;
-#pragma unroll 8
-            for (int t = 0; t < C; ++t) {
-                const int tt = t0 + t;
-                acc += tt < a.T ? gp[(int64_t)tt * a.g_st + c * a.g_sj] : 0.f;
-                sG[t * J + c] = acc;
-            }
-        }
-    }
-    __syncthreads();
-}
-
-// Copy one chunk of rows [t0, t0+C) x columns [col0, col0+W) into LDS
-// transposed ([W][pitch] 16-bit operands), scaled per element; with LO the
-// rounding remainder goes to dst_lo.
-template <int DT, int W, int PITCH, bool LO, typename Scale>
-__device__ void load_transposed(const typename Stor<DT>::type *base, int64_t row_stride, int col0, int t0, int T,
-                                uint16_t *dst, uint16_t *dst_lo, Scale scale) {
-    using in_t = typename Stor<DT>::type;
-    constexpr int NPIECE = (C / 2) * (W / 8);
-    for (int pi = threadIdx.x; pi < NPIECE; pi += NT) {
-        const int tp = pi / (W / 8), cc = pi % (W / 8);
-        const int t = 2 * tp;
-        float x[2][8];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int tt = t0 + t + r;
-            if (tt < T) {
-                const in_t *p = base + (int64_t)tt * row_stride + col0 + 8 * cc;
-                if constexpr (DT == HOFA_F32) {
-                    const f32x4 u = *(const f32x4 *)p, w = *(const f32x4 *)(p + 4);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        x[r][e] = u[e];
-                        x[r][4 + e] = w[e];
-                    }
-                } else {
-                    unpack16<DT>(*(const u32x4 *)p, x[r]);
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[r][e] = 0.f;
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) x[r][e] *= scale(t + r, 8 * cc + e);
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t hv = pack2<DT>(x[0][e], x[1][e]);
-            *(uint32_t *)&dst[(8 * cc + e) * PITCH + t] = hv;
-            if constexpr (LO)
-                *(uint32_t *)&dst_lo[(8 * cc + e) * PITCH + t] =
-                    pack2<DT>(x[0][e] - op_to_f32<DT>(hv & 0xffffu), x[1][e] - op_to_f32<DT>(hv >> 16));
-        }
-    }
-}
-
-template <int DT, int D, int J, bool GENERAL>
-__global__ __launch_bounds__(NT) void gla_state_kernel(GlaK a) {
-    using in_t = typename Stor<DT>::type;
-    constexpr int TP = C + 8;               // token pitch of the transposed tiles
-    constexpr bool VLO = DT == HOFA_F32;    // f32 inputs also split V
-    __shared__ float sG[C * J];
-    __shared__ float sAux[C + J];
-    __shared__ __attribute__((aligned(16))) uint16_t sKt[2][J * TP];
-    __shared__ __attribute__((aligned(16))) uint16_t sVt[VLO ? 2 : 1][D * TP];
-    const int bh = blockIdx.x / a.nc, c = blockIdx.x % a.nc;
-    const int b = bh / a.H, h = bh % a.H, t0 = c * C;
-    chunk_cumsum<J, GENERAL>(a, b, h, t0, sG, sAux);
-    const float *gl = sG + (C - 1) * J;
-    load_transposed<DT, J, TP, true>((const in_t *)a.k + b * a.k_sb + h * a.k_sh, a.k_st, a.R, t0, a.T, sKt[0],
-                                     sKt[1], [&](int t, int ch) { return fast_exp2((gl[ch] - sG[t * J + ch]) * kLog2e); });
-    load_transposed<DT, D, TP, VLO>((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, 0, t0, a.T, sVt[0],
-                                    sVt[VLO ? 1 : 0], [](int, int) { return 1.f; });
-    __syncthreads();
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int r16 = lane & 15, g4 = lane >> 4;
-    float *ds = a.ws_ds + ((int64_t)bh * a.nc + c) * D * J;
-    constexpr int NTILE = (D / 16) * (J / 16);
-    for (int tile = w; tile < NTILE; tile += NT / 64) {
-        const int tm = tile / (J / 16), tn = tile % (J / 16);
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < C / 32; ++ks) {
-            const int vo = (16 * tm + r16) * TP + 32 * ks + 8 * g4;
-            const int ko = (16 * tn + r16) * TP + 32 * ks + 8 * g4;
-            const u32x4 av = *(const u32x4 *)&sVt[0][vo];
-            acc = mfma16<DT>(av, *(const u32x4 *)&sKt[0][ko], acc);
-            acc = mfma16<DT>(av, *(const u32x4 *)&sKt[1][ko], acc);
-            if constexpr (VLO) acc = mfma16<DT>(*(const u32x4 *)&sVt[VLO ? 1 : 0][vo], *(const u32x4 *)&sKt[0][ko], acc);
-        }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) ds[(16 * tm + 4 * g4 + v) * J + 16 * tn + r16] = acc[v];
-    }
-    for (int ch = threadIdx.x; ch < J; ch += NT) a.ws_gl[((int64_t)bh * a.nc + c) * J + ch] = gl[ch];
-}
+using namespace gla;
+constexpr int NT = 128;  // threads of the output kernel
 
 template <int DT, int D, int J>
 __global__ __launch_bounds__(256) void gla_scan_kernel(GlaK a) {
@@ -180,12 +44,7 @@ __global__ __launch_bounds__(256) void gla_scan_kernel(GlaK a) {
     for (int c = 0; c < a.nc; ++c) {
         const f32x4 ds = *(const f32x4 *)(a.ws_ds + (base + c) * D * J + dv * J + j4);
         const f32x4 gl = *(const f32x4 *)(a.ws_gl + (base + c) * J + j4);
-        const uint2 hv = {pack2<DT>(S[0], S[1]), pack2<DT>(S[2], S[3])};
-        const uint2 lv = {pack2<DT>(S[0] - op_to_f32<DT>(hv.x & 0xffffu), S[1] - op_to_f32<DT>(hv.x >> 16)),
-                          pack2<DT>(S[2] - op_to_f32<DT>(hv.y & 0xffffu), S[3] - op_to_f32<DT>(hv.y >> 16))};
-        uint16_t *dst = a.s_in + (base + c) * 2 * D * J + dv * J + j4;
-        *(uint2 *)dst = hv;
-        *(uint2 *)(dst + D * J) = lv;
+        store_state_planes<DT, D, J>(a.s_in + (base + c) * a.nplanes * D * J, a.nplanes, dv, j4, S);
 #pragma unroll
         for (int e = 0; e < 4; ++e) S[e] = fmaf(fast_exp2(gl[e] * kLog2e), S[e], ds[e]);
     }
@@ -201,14 +60,14 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
     constexpr int VP = C + 4;
     constexpr int MB = D / 32;
     constexpr int KS = J / 16;
-    constexpr bool VLO = DT == HOFA_F32;  // f32 inputs also split V
+    constexpr bool VLO = kRawSplit<DT>;  // f32/f16 inputs also split V
     __shared__ float sG[C * J];
     __shared__ float sAux[C + J];
     __shared__ __attribute__((aligned(16))) uint16_t sVt[VLO ? 2 : 1][D * VP];
     const int bh = blockIdx.x / a.nc, c = blockIdx.x % a.nc;
     const int b = bh / a.H, h = bh % a.H, t0 = c * C;
-    chunk_cumsum<J, GENERAL>(a, b, h, t0, sG, sAux);
-    load_transposed<DT, D, VP, VLO>((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, 0, t0, a.T, sVt[0],
+    chunk_cumsum<J, GENERAL, NT>(a, b, h, t0, sG, sAux);
+    load_transposed<DT, D, VP, VLO, NT>((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, 0, t0, a.T, sVt[0],
                                     sVt[VLO ? 1 : 0], [](int, int) { return 1.f; });
     __syncthreads();
 
@@ -249,7 +108,7 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
         row8(qp, a.q_st, tq, ks, x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(sG[qi * J + 16 * ks + 8 * hi + e] * kLog2e);
-        split8<DT>(x, qh[ks], ql[ks]);
+        split8<OPB>(x, qh[ks], ql[ks]);
     }
 
     f32x16 y[MB];
@@ -271,10 +130,10 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(-sG[kj * J + 16 * ks + 8 * hi + e] * kLog2e);
                 u32x4 kh, kl;
-                split8<DT>(x, kh, kl);
-                at = mfma32<DT>(kh, qh[ks], at);
-                at = mfma32<DT>(kh, ql[ks], at);
-                at = mfma32<DT>(kl, qh[ks], at);
+                split8<OPB>(x, kh, kl);
+                at = mfma32<OPB>(kh, qh[ks], at);
+                at = mfma32<OPB>(kh, ql[ks], at);
+                at = mfma32<OPB>(kl, qh[ks], at);
             }
         } else {
             // element-wise: A[q, k] = sum_c q_c k_c exp(G_q,c - G_k,c), every exponent <= 0
@@ -301,34 +160,34 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2) {
             u32x4 ph, pl;
-            split8v<DT>(at, 8 * k2, ph, pl);
+            split8v<OPB>(at, 8 * k2, ph, pl);
             const int ks4 = 2 * kb + k2;
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const int vo = (32 * mb + (lane & 31)) * VP + 16 * ks4 + 4 * hi;
                 const uint2 lo = *(const uint2 *)&sVt[0][vo], hi8 = *(const uint2 *)&sVt[0][vo + 8];
                 const u32x4 va = {lo.x, lo.y, hi8.x, hi8.y};
-                y[mb] = mfma32<DT>(va, ph, y[mb]);
-                y[mb] = mfma32<DT>(va, pl, y[mb]);
+                y[mb] = mfma32<OPB>(va, ph, y[mb]);
+                y[mb] = mfma32<OPB>(va, pl, y[mb]);
                 if constexpr (VLO) {
                     const uint2 l2 = *(const uint2 *)&sVt[VLO ? 1 : 0][vo],
                                 h2 = *(const uint2 *)&sVt[VLO ? 1 : 0][vo + 8];
-                    y[mb] = mfma32<DT>(u32x4{l2.x, l2.y, h2.x, h2.y}, ph, y[mb]);
+                    y[mb] = mfma32<OPB>(u32x4{l2.x, l2.y, h2.x, h2.y}, ph, y[mb]);
                 }
             }
         }
     }
     if (c > 0) {  // inter-chunk term: S_in^T Q~^T
-        const uint16_t *sin = a.s_in + ((int64_t)bh * a.nc + c) * 2 * D * J;
+        const uint16_t *sin = a.s_in + ((int64_t)bh * a.nc + c) * a.nplanes * D * J;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const int so = (32 * mb + (lane & 31)) * J + 16 * ks + 8 * hi;
                 const u32x4 sh = *(const u32x4 *)(sin + so), sl = *(const u32x4 *)(sin + D * J + so);
-                y[mb] = mfma32<DT>(sh, qh[ks], y[mb]);
-                y[mb] = mfma32<DT>(sh, ql[ks], y[mb]);
-                y[mb] = mfma32<DT>(sl, qh[ks], y[mb]);
+                y[mb] = mfma32<OPB>(sh, qh[ks], y[mb]);
+                y[mb] = mfma32<OPB>(sh, ql[ks], y[mb]);
+                y[mb] = mfma32<OPB>(sl, qh[ks], y[mb]);
             }
     }
 
@@ -344,6 +203,14 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
         const float mixv =
             tq < a.T ? load_any(a.mix, a.mix_dt, b * a.m_sb + h * a.m_sh + (int64_t)tq * a.m_st) : 0.f;
         const float f = (1.f - mixv) * rs;
+        if (a.n_out && tq < a.T) {  // RMSNorm(Y_I) and 1/rms, saved for the backward pass
+            in_t *nr = (in_t *)a.n_out + b * a.n_sb + h * a.n_sh + (int64_t)tq * a.n_st;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) nr[32 * mb + 8 * (v / 4) + 4 * hi + (v % 4)] = from_f32<DT>(y[mb][v] * rs);
+            if (hi == 0) a.rstd[(int64_t)bh * a.T + tq] = rs;
+        }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -405,13 +272,15 @@ int validate(const hofa_gla_fwd_args_t *a) {
     HOFA_REQUIRE(!a->fuse_norm_gate || (a->mix.data && a->gla_scale.data), HOFA_EINVAL,
                  "hofa_gla_fwd: fuse_norm_gate needs mix and gla_scale");
     HOFA_REQUIRE(a->state_out.dtype == HOFA_F32, HOFA_EINVAL, "hofa_gla_fwd: state_out must be float32");
+    HOFA_REQUIRE(!a->n_out.data || (a->fuse_norm_gate && a->rstd && a->n_out.dtype == dt && rows_ok(a->n_out, es)),
+                 HOFA_EINVAL, "hofa_gla_fwd: n_out needs fuse_norm_gate, rstd, the dtype of y and aligned rows");
     return HOFA_OK;
 }
 
 template <int DT, int D, int J, bool GEN>
 void launch(const GlaK &k, hipStream_t s) {
     const int nblk = k.B * k.H * k.nc;
-    hipLaunchKernelGGL((gla_state_kernel<DT, D, J, GEN>), dim3(nblk), dim3(NT), 0, s, k);
+    hipLaunchKernelGGL((gla_state_kernel<DT, D, J, GEN, false>), dim3(nblk), dim3(kStateThreads), 0, s, k);
     hipLaunchKernelGGL((gla_scan_kernel<DT, D, J>), dim3(k.B * k.H, (D * J / 4 + 255) / 256), dim3(256), 0, s, k);
     hipLaunchKernelGGL((gla_out_kernel<DT, D, J, GEN>), dim3(nblk), dim3(NT), 0, s, k);
 }
@@ -458,6 +327,10 @@ extern "C" int hofa_gla_fwd(const hofa_gla_fwd_args_t *a, void *workspace, size_
     k.ws_ds = (float *)(w + L.ds);
     k.ws_gl = (float *)(w + L.gl);
     k.s_in = a->chunk_states ? (uint16_t *)a->chunk_states : (uint16_t *)(w + L.sin);
+    k.nplanes = a->chunk_states ? 4 : 2;
+    k.n_out = (void *)a->n_out.data;
+    k.rstd = a->n_out.data ? a->rstd : nullptr;
+    k.n_sb = a->n_out.stride[0]; k.n_sh = a->n_out.stride[1]; k.n_st = a->n_out.stride[2];
     k.q_sb = a->q.stride[0]; k.q_sh = a->q.stride[1]; k.q_st = a->q.stride[2];
     k.k_sb = a->k.stride[0]; k.k_sh = a->k.stride[1]; k.k_st = a->k.stride[2];
     k.v_sb = a->v.stride[0]; k.v_sh = a->v.stride[1]; k.v_st = a->v.stride[2];
@@ -472,6 +345,7 @@ extern "C" int hofa_gla_fwd(const hofa_gla_fwd_args_t *a, void *workspace, size_
     k.lg_dt = a->log_gamma.dtype; k.la_dt = a->log_alpha.dtype; k.mix_dt = a->mix.dtype; k.gs_dt = a->gla_scale.dtype;
     k.B = a->B; k.H = a->H; k.T = a->T; k.R = a->R;
     k.nc = (a->T + C - 1) / C;
+    k.key_col0 = a->R;
     k.fuse = a->fuse_norm_gate;
     k.eps = a->eps;
     const int J = a->D - a->R;

@@ -1,0 +1,871 @@
+// Backward of the inlier pathway (chunked GLA) and of the fused
+// RMSNorm / gla_scale / mix epilogue, for gfx950.
+//
+// No reference kernel: the reference trains through autograd of fla's
+// chunk_gla, nn.RMSNorm, the gla_scale product and torch.lerp
+// (src/HybridOutlierFactorizedAttentionTrain.py:263-294).  Forward, per head:
+//   S_t = diag(exp(g_t)) S_{t-1} + k_t^T v_t,  Y_I[t] = q_t S_t
+//   N = Y_I * rstd,  Y = (1 - m) gs N + m O
+// Gradients, with G the in-chunk inclusive cumsum of g, Q~ = q e^G,
+// K~ = k e^-G, K^ = k e^(G_last - G), M = dO V^T and A = Q~ K~^T (both
+// masked to key <= query inside the chunk):
+//   dN = (1 - m) gs dY,  dO = rstd (dN - N mean(dN N)),  dm = sum_d dY (O - gs N)
+//   dH_end(c) = Q~(c+1)^T dO(c+1) + e^(G_last(c+1)) dH_end(c+1)     (reverse scan)
+//   dq = e^G (M K~ + dO S_in^T)
+//   dk = e^-G (M^T Q~) + e^(G_last - G) (V dH_end^T)
+//   dv = A^T dO + K^ dH_end
+//   dGamma = q dq - k dk   (gradient of the global cumsum of g), so
+//   d log_gamma_t = sum_{s >= t} sum_c a_c dGamma_sc            (a = exp(log_alpha))
+//   d log_alpha_c = a_c sum_s dGamma_sc Lambda_s                 (Lambda = cumsum log_gamma)
+//   d g_tc        = sum_{s >= t} dGamma_sc                        (general decay)
+// Launches:
+//   1. gla_bwd_epilogue_kernel  per token: dO (gradient of Y_I), d_mix, mix*dY,
+//                               delta = rowsum(mix dY O), gla_scale partials
+//   2. gla_state_kernel<BWD>    per chunk: dH^T = dO^T Q~ (shared with the forward)
+//   3. gla_bwd_scan_kernel      reverse element-wise scan -> dH_end(c) as hi/lo planes
+//   4. gla_bwd_chunk_kernel     per chunk, 4 waves: 2 key-side waves (dk, dv),
+//                               2 query-side waves (dq); dGamma reductions
+//   5. gla_bwd_dlg_kernel       per head: later-chunk suffix of d log_gamma / d g
+//   6. gla_bwd_param_kernel     per head: d gla_scale, d log_alpha
+// Every matrix-core product takes bf16 operands; computed operands are hi/lo
+// pairs (see split8) and raw f32/f16 inputs are split too, so products track fp32.
+#include "hofa_gla_common.h"
+
+namespace hofa {
+namespace {
+
+using namespace gla;
+
+constexpr int NTB = 256;   // threads of the chunk backward kernel
+constexpr int ET = 256;    // tokens per epilogue block
+constexpr int kMaxChunks = 4096;
+
+struct GlaBwdK {
+    GlaK f;  // forward inputs: q, k, v, lg, la, g, mix, gs with strides; B, H, T, R, nc
+    const void *dy, *n, *o;
+    const float *rstd;
+    const uint16_t *s_in;  // chunk_states, four planes
+    void *dq, *dk, *dv, *dlg, *dg, *dla, *dmix, *dgs, *dout;
+    float *delta;
+    int64_t dy_sb, dy_sh, dy_st, n_sb, n_sh, n_st, o_sb, o_sh, o_st;
+    int64_t dq_sb, dq_sh, dq_st, dk_sb, dk_sh, dk_st, dv_sb, dv_sh, dv_st;
+    int64_t dlg_sb, dlg_sh, dlg_st, dg_sb, dg_sh, dg_st, dg_sj, dla_sh, dla_sj;
+    int64_t dmix_sb, dmix_sh, dmix_st, dgs_sh, dgs_sd, do_sb, do_sh, do_st;
+    int dlg_dt, dla_dt, dmix_dt, dgs_dt;
+    void *ws_do;        // [B*H][T][D] (dtype of q): gradient of Y_I
+    float *ws_dh;       // [B*H][nc][D][J]
+    float *ws_gl;       // [B*H][nc][J]
+    uint16_t *ds_end;   // [B*H][nc][4][D*J]
+    float *dlg_part;    // [B*H][T]
+    float *chunk_part;  // [B*H][nc][2J+2]: sum_t dGamma, sum_t dGamma*Lin, e-total, log_gamma total
+    float *dgs_part;    // [B*H][ntile][D]
+    int ntile;
+};
+
+// 8 consecutive elements of row t starting at column col, as floats (0 past T).
+template <int DT>
+__device__ __forceinline__ void row8f(const typename Stor<DT>::type *base, int64_t st, int t, int T, int col,
+                                      float *x) {
+    if (t < T) {
+        const typename Stor<DT>::type *p = base + (int64_t)t * st + col;
+        if constexpr (DT == HOFA_F32) {
+            const f32x4 u = *(const f32x4 *)p, v = *(const f32x4 *)(p + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[e] = u[e];
+                x[4 + e] = v[e];
+            }
+        } else {
+            unpack16<DT>(*(const u32x4 *)p, x);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = 0.f;
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void store8(typename Stor<DT>::type *p, const float *x) {
+    if constexpr (DT == HOFA_F32) {
+        *(f32x4 *)p = f32x4{x[0], x[1], x[2], x[3]};
+        *(f32x4 *)(p + 4) = f32x4{x[4], x[5], x[6], x[7]};
+    } else {
+        *(u32x4 *)p = pack8<DT>(x);
+    }
+}
+
+// A operand of a k-step of 16 along the permuted index of a C-layout tile
+// (entries [16ks + 4hi .. +3] and [16ks + 8 + 4hi .. +3] of an LDS row).
+__device__ __forceinline__ u32x4 perm_a(const uint16_t *row, int ks, int hi) {
+    const uint16_t *p = row + 16 * ks + 4 * hi;
+    const uint2 lo = *(const uint2 *)p, h8 = *(const uint2 *)(p + 8);
+    return u32x4{lo.x, lo.y, h8.x, h8.y};
+}
+
+// Row of the v-th accumulator entry of a 32x32 C-layout tile.
+__device__ __forceinline__ int crow(int v, int hi) { return 8 * (v / 4) + 4 * hi + (v % 4); }
+
+// ---------------------------------------------------------------- 1. epilogue
+template <int DT, int D>
+__global__ __launch_bounds__(256) void gla_bwd_epilogue_kernel(GlaBwdK a) {
+    using in_t = typename Stor<DT>::type;
+    constexpr int LPR = D / 8;      // lanes per token row
+    constexpr int RPP = 256 / LPR;  // rows per pass
+    __shared__ float sP[256][9];
+    const int bh = blockIdx.x, tile = blockIdx.y;
+    const int H = a.f.H, T = a.f.T;
+    const int b = bh / H, h = bh % H;
+    const int tid = threadIdx.x, slot = tid % LPR, r = tid / LPR, d0 = 8 * slot;
+    float gsv[8], part[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        gsv[e] = load_any(a.f.gs, a.f.gs_dt, h * a.f.gs_sh + (d0 + e) * a.f.gs_sd);
+        part[e] = 0.f;
+    }
+    auto group_sum = [](float x) {
+#pragma unroll
+        for (int off = LPR / 2; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+        return x;
+    };
+    for (int pass = 0; pass < ET / RPP; ++pass) {
+        const int t = tile * ET + pass * RPP + r;
+        if (t >= T) break;  // whole row groups leave together
+        float dy[8], nv[8], ov[8];
+        row8f<DT>((const in_t *)a.dy + b * a.dy_sb + h * a.dy_sh, a.dy_st, t, T, d0, dy);
+        row8f<DT>((const in_t *)a.n + b * a.n_sb + h * a.n_sh, a.n_st, t, T, d0, nv);
+        if (a.o) {
+            row8f<DT>((const in_t *)a.o + b * a.o_sb + h * a.o_sh, a.o_st, t, T, d0, ov);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ov[e] = 0.f;
+        }
+        const float m = a.f.mix ? load_any(a.f.mix, a.f.mix_dt, b * a.f.m_sb + h * a.f.m_sh + (int64_t)t * a.f.m_st) : 0.f;
+        const float rs = a.rstd[(int64_t)bh * T + t];
+        float dn[8], snn = 0.f, syo = 0.f, syn = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float dyi = (1.f - m) * dy[e];
+            dn[e] = gsv[e] * dyi;
+            part[e] = fmaf(dyi, nv[e], part[e]);
+            snn = fmaf(dn[e], nv[e], snn);
+            syo = fmaf(dy[e], ov[e], syo);
+            syn = fmaf(dy[e], gsv[e] * nv[e], syn);
+        }
+        snn = group_sum(snn) / (float)D;
+        syo = group_sum(syo);
+        syn = group_sum(syn);
+        float dov[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dov[e] = rs * (dn[e] - nv[e] * snn);
+        store8<DT>((in_t *)a.ws_do + ((int64_t)bh * T + t) * D + d0, dov);
+        if (a.dout) {
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = m * dy[e];
+            store8<DT>((in_t *)a.dout + b * a.do_sb + h * a.do_sh + (int64_t)t * a.do_st + d0, x);
+        }
+        if (slot == 0) {
+            if (a.delta) a.delta[(int64_t)bh * T + t] = m * syo;
+            if (a.dmix) store_any(a.dmix, a.dmix_dt, b * a.dmix_sb + h * a.dmix_sh + (int64_t)t * a.dmix_st, syo - syn);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sP[tid][e] = part[e];
+    __syncthreads();
+    for (int d = tid; d < D; d += 256) {
+        float s = 0.f;
+        for (int rr = 0; rr < RPP; ++rr) s += sP[rr * LPR + d / 8][d % 8];
+        a.dgs_part[((int64_t)bh * a.ntile + tile) * D + d] = s;
+    }
+}
+
+// ---------------------------------------------------------------- 3. reverse scan
+template <int DT, int D, int J>
+__global__ __launch_bounds__(256) void gla_bwd_scan_kernel(GlaBwdK a) {
+    const int bh = blockIdx.x;
+    const int idx = blockIdx.y * 256 + threadIdx.x;
+    if (idx >= D * J / 4) return;
+    const int dv = idx / (J / 4), j4 = (idx % (J / 4)) * 4;
+    const int nc = a.f.nc;
+    const int64_t base = (int64_t)bh * nc;
+    f32x4 X = {0.f, 0.f, 0.f, 0.f};
+    for (int c = nc - 1; c >= 0; --c) {
+        store_state_planes<DT, D, J>(a.ds_end + (base + c) * 4 * D * J, 4, dv, j4, X);
+        const f32x4 dh = *(const f32x4 *)(a.ws_dh + (base + c) * D * J + dv * J + j4);
+        const f32x4 gl = *(const f32x4 *)(a.ws_gl + (base + c) * J + j4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) X[e] = fmaf(fast_exp2(gl[e] * kLog2e), X[e], dh[e]);
+    }
+}
+
+// ---------------------------------------------------------------- 4. chunk kernel
+template <int DT, int D, int J, bool GENERAL>
+__global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
+    using in_t = typename Stor<DT>::type;
+    constexpr int TP = C + 4;             // token pitch of the transposed tiles
+    constexpr int JB = (J + 31) / 32;     // 32-row channel blocks
+    constexpr int JP = 32 * JB;
+    constexpr int KS = J / 16;
+    constexpr int DKS = D / 16;
+    constexpr int MB = D / 32;
+    constexpr bool SPL = kRawSplit<DT>;   // raw f32/f16 inputs are split as well
+    constexpr int NO = SPL ? 2 : 1;
+    __shared__ float sG[C * J];
+    __shared__ float sAux[C + J];
+    __shared__ __attribute__((aligned(16))) uint16_t sQK[2][2][JP * TP];  // [Q~^T | K~^T][hi | lo]
+    __shared__ __attribute__((aligned(16))) uint16_t sOt[NO][D * TP];     // dO^T
+    static_assert(sizeof(sQK) >= sizeof(float) * C * J, "dGamma reuses the operand tiles");
+
+    const int nc = a.f.nc, H = a.f.H, T = a.f.T, R = a.f.R;
+    const int bh = blockIdx.x / nc, c = blockIdx.x % nc;
+    const int b = bh / H, h = bh % H, t0 = c * C;
+    chunk_cumsum<J, GENERAL, NTB>(a.f, b, h, t0, sG, sAux);
+    const in_t *qp = (const in_t *)a.f.q + b * a.f.q_sb + h * a.f.q_sh;
+    const in_t *kp = (const in_t *)a.f.k + b * a.f.k_sb + h * a.f.k_sh;
+    const in_t *vp = (const in_t *)a.f.v + b * a.f.v_sb + h * a.f.v_sh;
+    const in_t *dop = (const in_t *)a.ws_do + (int64_t)bh * T * D;
+    load_transposed<DT, J, TP, true, NTB>(qp, a.f.q_st, R, t0, T, sQK[0][0], sQK[0][1],
+                                          [&](int t, int ch) { return fast_exp2(sG[t * J + ch] * kLog2e); });
+    load_transposed<DT, J, TP, true, NTB>(kp, a.f.k_st, R, t0, T, sQK[1][0], sQK[1][1],
+                                          [&](int t, int ch) { return fast_exp2(-sG[t * J + ch] * kLog2e); });
+    load_transposed<DT, D, TP, SPL, NTB>(dop, D, 0, t0, T, sOt[0], sOt[NO - 1], [](int, int) { return 1.f; });
+    if constexpr (JP > J) {
+        for (int i = threadIdx.x; i < (JP - J) * TP; i += NTB) {
+            sQK[0][0][J * TP + i] = 0;
+            sQK[0][1][J * TP + i] = 0;
+            sQK[1][0][J * TP + i] = 0;
+            sQK[1][1][J * TP + i] = 0;
+        }
+    }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63, hi = lane >> 5, l32 = lane & 31;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float range = 0.f;
+    for (int idx = lane; idx < C * J; idx += 64) range = fmaxf(range, fabsf(sG[idx]));
+    const bool safe = wave_max(range) <= kSafeRange;
+    const float *gl = sG + (C - 1) * J;
+    const uint16_t *sin = a.s_in + ((int64_t)bh * nc + c) * 4 * D * J;
+    const uint16_t *dse = a.ds_end + ((int64_t)bh * nc + c) * 4 * D * J;
+    auto qval = [&](int ti, int ch) { return t0 + ti < T ? to_f32<DT>(qp[(int64_t)(t0 + ti) * a.f.q_st + R + ch]) : 0.f; };
+    auto kval = [&](int ti, int ch) { return t0 + ti < T ? to_f32<DT>(kp[(int64_t)(t0 + ti) * a.f.k_st + R + ch]) : 0.f; };
+    const u32x4 zero4 = {0, 0, 0, 0};
+
+    f32x16 acc[JB];  // dk^T (key side) or dq^T (query side): rows = channel, col = token
+#pragma unroll
+    for (int jb = 0; jb < JB; ++jb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[jb][v] = 0.f;
+    int tok;  // chunk-relative token of this lane's column
+
+    if (w < 2) {
+        // ================= key side: keys s = 32w + l32
+        const int kb = w, s = 32 * kb + l32, ts = t0 + s;
+        tok = s;
+        f32x16 dvt[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) dvt[mb][v] = 0.f;
+        u32x4 vh[DKS], vl[DKS];
+#pragma unroll
+        for (int ks = 0; ks < DKS; ++ks) {
+            vh[ks] = vl[ks] = zero4;
+            if (ts < T) raw_op8<DT>(vp + (int64_t)ts * a.f.v_st + 16 * ks + 8 * hi, vh[ks], vl[ks]);
+        }
+        u32x4 kth[KS], ktl[KS];  // K~ = k e^-G of this key
+        if (safe) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                float x[8];
+                row8f<DT>(kp, a.f.k_st, ts, T, R + 16 * ks + 8 * hi, x);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(-sG[s * J + 16 * ks + 8 * hi + e] * kLog2e);
+                split8<OPB>(x, kth[ks], ktl[ks]);
+            }
+        }
+        for (int tb = kb; tb < 2; ++tb) {
+            const int tr = 32 * tb + l32;  // A-operand row (query) of this lane
+            f32x16 mt, at;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                mt[v] = 0.f;
+                at[v] = 0.f;
+            }
+            // M[t, s] = sum_d dO[t, d] V[s, d]
+#pragma unroll
+            for (int ks = 0; ks < DKS; ++ks) {
+                u32x4 oh = zero4, ol = zero4;
+                if (t0 + tr < T) raw_op8<DT>(dop + (int64_t)(t0 + tr) * D + 16 * ks + 8 * hi, oh, ol);
+                mt = mfma32<OPB>(oh, vh[ks], mt);
+                if constexpr (SPL) {
+                    mt = mfma32<OPB>(oh, vl[ks], mt);
+                    mt = mfma32<OPB>(ol, vh[ks], mt);
+                }
+            }
+            // A[t, s] = sum_c q_tc k_sc e^(G_tc - G_sc)
+            if (safe) {
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    float x[8];
+                    row8f<DT>(qp, a.f.q_st, t0 + tr, T, R + 16 * ks + 8 * hi, x);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(sG[tr * J + 16 * ks + 8 * hi + e] * kLog2e);
+                    u32x4 qh, ql;
+                    split8<OPB>(x, qh, ql);
+                    at = mfma32<OPB>(qh, kth[ks], at);
+                    at = mfma32<OPB>(qh, ktl[ks], at);
+                    at = mfma32<OPB>(ql, kth[ks], at);
+                }
+            } else {
+                for (int ch = 0; ch < J; ++ch) {
+                    const float kv = kval(s, ch), gs_ = sG[s * J + ch];
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int ti = 32 * tb + crow(v, hi);
+                        if (ti >= s) at[v] = fmaf(qval(ti, ch) * kv, fast_exp2((sG[ti * J + ch] - gs_) * kLog2e), at[v]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                if (32 * tb + crow(v, hi) < s) {
+                    mt[v] = 0.f;
+                    at[v] = 0.f;
+                }
+            }
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                const int ks4 = 2 * tb + k2;
+                u32x4 ah, al;
+                split8v<OPB>(at, 8 * k2, ah, al);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    const int ro = (32 * mb + l32) * TP;
+                    const u32x4 oa = perm_a(&sOt[0][ro], ks4, hi);
+                    dvt[mb] = mfma32<OPB>(oa, ah, dvt[mb]);
+                    dvt[mb] = mfma32<OPB>(oa, al, dvt[mb]);
+                    if constexpr (SPL) dvt[mb] = mfma32<OPB>(perm_a(&sOt[NO - 1][ro], ks4, hi), ah, dvt[mb]);
+                }
+                if (safe) {
+                    u32x4 mh, ml;
+                    split8v<OPB>(mt, 8 * k2, mh, ml);
+#pragma unroll
+                    for (int jb = 0; jb < JB; ++jb) {
+                        const int ro = (32 * jb + l32) * TP;
+                        const u32x4 qa = perm_a(&sQK[0][0][ro], ks4, hi), qal = perm_a(&sQK[0][1][ro], ks4, hi);
+                        acc[jb] = mfma32<OPB>(qa, mh, acc[jb]);
+                        acc[jb] = mfma32<OPB>(qa, ml, acc[jb]);
+                        acc[jb] = mfma32<OPB>(qal, mh, acc[jb]);
+                    }
+                }
+            }
+            if (!safe) {  // dk_sc += sum_t M[t, s] q_tc e^(G_tc - G_sc) over the tile's rows (both lane halves)
+                f32x16 mo;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) mo[v] = __shfl_xor(mt[v], 32);
+#pragma unroll
+                for (int jb = 0; jb < JB; ++jb)
+#pragma unroll
+                    for (int vv = 0; vv < 16; ++vv) {
+                        const int ch = 32 * jb + crow(vv, hi);
+                        if (ch >= J) continue;
+                        const float gsc = sG[s * J + ch];
+                        float x = 0.f;
+                        for (int v = 0; v < 16; ++v) {
+                            const int ta = 32 * tb + crow(v, hi), tbb = 32 * tb + crow(v, 1 - hi);
+                            if (ta >= s) x = fmaf(mt[v] * qval(ta, ch), fast_exp2((sG[ta * J + ch] - gsc) * kLog2e), x);
+                            if (tbb >= s) x = fmaf(mo[v] * qval(tbb, ch), fast_exp2((sG[tbb * J + ch] - gsc) * kLog2e), x);
+                        }
+                        acc[jb][vv] += x;
+                    }
+            }
+        }
+        if (safe) {
+#pragma unroll
+            for (int jb = 0; jb < JB; ++jb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int ch = 32 * jb + crow(v, hi);
+                    acc[jb][v] = ch < J ? acc[jb][v] * fast_exp2(-sG[s * J + ch] * kLog2e) : 0.f;
+                }
+        }
+        if (c < nc - 1) {  // state gradient from later chunks
+            // dk^T[c, s] += e^(G_last,c - G_sc) sum_d dH_end[c, d] V[s, d]
+#pragma unroll
+            for (int jb = 0; jb < JB; ++jb) {
+                const int cr = 32 * jb + l32;
+                f32x16 x;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) x[v] = 0.f;
+#pragma unroll
+                for (int ks = 0; ks < DKS; ++ks) {
+                    const int off = cr * D + 16 * ks + 8 * hi;
+                    const u32x4 sh = cr < J ? *(const u32x4 *)(dse + 2 * D * J + off) : zero4;
+                    const u32x4 sl = cr < J ? *(const u32x4 *)(dse + 3 * D * J + off) : zero4;
+                    x = mfma32<OPB>(sh, vh[ks], x);
+                    x = mfma32<OPB>(sl, vh[ks], x);
+                    if constexpr (SPL) x = mfma32<OPB>(sh, vl[ks], x);
+                }
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int ch = 32 * jb + crow(v, hi);
+                    if (ch < J) acc[jb][v] = fmaf(fast_exp2((gl[ch] - sG[s * J + ch]) * kLog2e), x[v], acc[jb][v]);
+                }
+            }
+            // dv^T[d, s] += sum_c dH_end^T[d, c] K^[s, c]
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                float x[8];
+                row8f<DT>(kp, a.f.k_st, ts, T, R + 16 * ks + 8 * hi, x);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int ch = 16 * ks + 8 * hi + e;
+                    x[e] *= fast_exp2((gl[ch] - sG[s * J + ch]) * kLog2e);
+                }
+                u32x4 kh, kl;
+                split8<OPB>(x, kh, kl);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    const int off = (32 * mb + l32) * J + 16 * ks + 8 * hi;
+                    const u32x4 sh = *(const u32x4 *)(dse + off), sl = *(const u32x4 *)(dse + D * J + off);
+                    dvt[mb] = mfma32<OPB>(sh, kh, dvt[mb]);
+                    dvt[mb] = mfma32<OPB>(sh, kl, dvt[mb]);
+                    dvt[mb] = mfma32<OPB>(sl, kh, dvt[mb]);
+                }
+            }
+        }
+        if (ts < T) {
+            in_t *dkr = (in_t *)a.dk + b * a.dk_sb + h * a.dk_sh + (int64_t)ts * a.dk_st + R;
+            in_t *dvr = (in_t *)a.dv + b * a.dv_sb + h * a.dv_sh + (int64_t)ts * a.dv_st;
+#pragma unroll
+            for (int jb = 0; jb < JB; ++jb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int ch = 32 * jb + crow(v, hi);
+                    if (ch < J) dkr[ch] = from_f32<DT>(acc[jb][v]);
+                }
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) dvr[32 * mb + crow(v, hi)] = from_f32<DT>(dvt[mb][v]);
+        }
+    } else {
+        // ================= query side: queries t = 32(w-2) + l32
+        const int qb = w - 2, t = 32 * qb + l32, tq = t0 + t;
+        tok = t;
+        u32x4 dh[DKS], dl[DKS];
+#pragma unroll
+        for (int ks = 0; ks < DKS; ++ks) {
+            dh[ks] = dl[ks] = zero4;
+            if (tq < T) raw_op8<DT>(dop + (int64_t)tq * D + 16 * ks + 8 * hi, dh[ks], dl[ks]);
+        }
+        for (int sb = 0; sb <= qb; ++sb) {
+            const int sr = 32 * sb + l32;  // A-operand row (key) of this lane
+            f32x16 mt;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) mt[v] = 0.f;
+            // M^T[s, t] = sum_d V[s, d] dO[t, d]
+#pragma unroll
+            for (int ks = 0; ks < DKS; ++ks) {
+                u32x4 va = zero4, vla = zero4;
+                if (t0 + sr < T) raw_op8<DT>(vp + (int64_t)(t0 + sr) * a.f.v_st + 16 * ks + 8 * hi, va, vla);
+                mt = mfma32<OPB>(va, dh[ks], mt);
+                if constexpr (SPL) {
+                    mt = mfma32<OPB>(va, dl[ks], mt);
+                    mt = mfma32<OPB>(vla, dh[ks], mt);
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                if (32 * sb + crow(v, hi) > t) mt[v] = 0.f;
+            if (safe) {
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2) {
+                    const int ks4 = 2 * sb + k2;
+                    u32x4 mh, ml;
+                    split8v<OPB>(mt, 8 * k2, mh, ml);
+#pragma unroll
+                    for (int jb = 0; jb < JB; ++jb) {
+                        const int ro = (32 * jb + l32) * TP;
+                        const u32x4 ka = perm_a(&sQK[1][0][ro], ks4, hi), kal = perm_a(&sQK[1][1][ro], ks4, hi);
+                        acc[jb] = mfma32<OPB>(ka, mh, acc[jb]);
+                        acc[jb] = mfma32<OPB>(ka, ml, acc[jb]);
+                        acc[jb] = mfma32<OPB>(kal, mh, acc[jb]);
+                    }
+                }
+            } else {  // dq_tc += sum_s M[t, s] k_sc e^(G_tc - G_sc)
+                f32x16 mo;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) mo[v] = __shfl_xor(mt[v], 32);
+#pragma unroll
+                for (int jb = 0; jb < JB; ++jb)
+#pragma unroll
+                    for (int vv = 0; vv < 16; ++vv) {
+                        const int ch = 32 * jb + crow(vv, hi);
+                        if (ch >= J) continue;
+                        const float gtc = sG[t * J + ch];
+                        float x = 0.f;
+                        for (int v = 0; v < 16; ++v) {
+                            const int sa = 32 * sb + crow(v, hi), sbb = 32 * sb + crow(v, 1 - hi);
+                            if (sa <= t) x = fmaf(mt[v] * kval(sa, ch), fast_exp2((gtc - sG[sa * J + ch]) * kLog2e), x);
+                            if (sbb <= t) x = fmaf(mo[v] * kval(sbb, ch), fast_exp2((gtc - sG[sbb * J + ch]) * kLog2e), x);
+                        }
+                        acc[jb][vv] += x;
+                    }
+            }
+        }
+        // dq^T[c, t] (+)= e^G_tc (sum_d S_in[c, d] dO[t, d])
+#pragma unroll
+        for (int jb = 0; jb < JB; ++jb) {
+            const int cr = 32 * jb + l32;
+            f32x16 x;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) x[v] = 0.f;
+            if (c > 0) {
+#pragma unroll
+                for (int ks = 0; ks < DKS; ++ks) {
+                    const int off = cr * D + 16 * ks + 8 * hi;
+                    const u32x4 sh = cr < J ? *(const u32x4 *)(sin + 2 * D * J + off) : zero4;
+                    const u32x4 sl = cr < J ? *(const u32x4 *)(sin + 3 * D * J + off) : zero4;
+                    x = mfma32<OPB>(sh, dh[ks], x);
+                    x = mfma32<OPB>(sl, dh[ks], x);
+                    if constexpr (SPL) x = mfma32<OPB>(sh, dl[ks], x);
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int ch = 32 * jb + crow(v, hi);
+                const float eg = ch < J ? fast_exp2(sG[t * J + ch] * kLog2e) : 0.f;
+                acc[jb][v] = safe ? eg * (acc[jb][v] + x[v]) : fmaf(eg, x[v], acc[jb][v]);
+            }
+        }
+        if (tq < T) {
+            in_t *dqr = (in_t *)a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)tq * a.dq_st + R;
+#pragma unroll
+            for (int jb = 0; jb < JB; ++jb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int ch = 32 * jb + crow(v, hi);
+                    if (ch < J) dqr[ch] = from_f32<DT>(acc[jb][v]);
+                }
+        }
+    }
+
+    // ---- dGamma = q dq - k dk in LDS (reusing the operand tiles)
+    __syncthreads();
+    float *sDG = (float *)&sQK[0][0][0];
+    if (w >= 2) {
+#pragma unroll
+        for (int jb = 0; jb < JB; ++jb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int ch = 32 * jb + crow(v, hi);
+                if (ch < J) sDG[tok * J + ch] = qval(tok, ch) * acc[jb][v];
+            }
+    }
+    __syncthreads();
+    if (w < 2) {
+#pragma unroll
+        for (int jb = 0; jb < JB; ++jb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int ch = 32 * jb + crow(v, hi);
+                if (ch < J) sDG[tok * J + ch] -= kval(tok, ch) * acc[jb][v];
+            }
+    }
+    __syncthreads();
+    float *cp = a.chunk_part + ((int64_t)bh * nc + c) * (2 * J + 2);
+    if constexpr (!GENERAL) {
+        const float *sLam = sAux, *sAl = sAux + C;
+        if (w == 0) {
+            float e = 0.f;
+            for (int ch = 0; ch < J; ++ch) e = fmaf(sAl[ch], sDG[lane * J + ch], e);
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float y = __shfl_down(e, off);
+                if (lane + off < 64) e += y;
+            }
+            if (t0 + lane < T) a.dlg_part[(int64_t)bh * T + t0 + lane] = e;
+            if (lane == 0) {
+                cp[2 * J] = e;
+                cp[2 * J + 1] = sLam[C - 1];
+            }
+        }
+        for (int ch = threadIdx.x; ch < J; ch += NTB) {
+            float ed = 0.f, f = 0.f;
+            for (int t = 0; t < C; ++t) {
+                const float x = sDG[t * J + ch];
+                ed += x;
+                f = fmaf(x, sLam[t], f);
+            }
+            cp[ch] = ed;
+            cp[J + ch] = f;
+        }
+    } else {
+        float *dg = (float *)a.dg + b * a.dg_sb + h * a.dg_sh;
+        for (int ch = threadIdx.x; ch < J; ch += NTB) {
+            float s = 0.f;
+            for (int t = C - 1; t >= 0; --t) {
+                s += sDG[t * J + ch];
+                if (t0 + t < T) dg[(int64_t)(t0 + t) * a.dg_st + ch * a.dg_sj] = s;
+            }
+            cp[ch] = s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- 5. later-chunk suffix
+template <int J, bool GENERAL>
+__global__ __launch_bounds__(256) void gla_bwd_dlg_kernel(GlaBwdK a) {
+    __shared__ float sSfx[kMaxChunks];
+    const int bh = blockIdx.x, H = a.f.H, T = a.f.T, nc = a.f.nc;
+    const int b = bh / H, h = bh % H;
+    const int tid = threadIdx.x, lane = tid & 63;
+    float *cp = a.chunk_part + (int64_t)bh * nc * (2 * J + 2);
+    if constexpr (!GENERAL) {
+        if (tid < 64) {
+            float carry = 0.f;
+            for (int top = nc - 1; top >= 0; top -= 64) {
+                const int c = top - lane;
+                const float e = c >= 0 ? cp[(int64_t)c * (2 * J + 2) + 2 * J] : 0.f;
+                float x = e;
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1) {
+                    const float y = __shfl_up(x, off);
+                    if (lane >= off) x += y;
+                }
+                if (c >= 0) sSfx[c] = carry + x - e;
+                carry += __shfl(x, 63);
+            }
+        }
+        __syncthreads();
+        for (int t = tid; t < T; t += 256)
+            store_any(a.dlg, a.dlg_dt, b * a.dlg_sb + h * a.dlg_sh + (int64_t)t * a.dlg_st,
+                      a.dlg_part[(int64_t)bh * T + t] + sSfx[t / C]);
+    } else {
+        for (int ch = tid; ch < J; ch += 256) {
+            float carry = 0.f;
+            for (int c = nc - 1; c >= 0; --c) {
+                float *p = cp + (int64_t)c * (2 * J + 2) + ch;
+                const float x = *p;
+                *p = carry;
+                carry += x;
+            }
+        }
+        __syncthreads();
+        float *dg = (float *)a.dg + b * a.dg_sb + h * a.dg_sh;
+        for (int64_t i = tid; i < (int64_t)T * J; i += 256) {
+            const int t = (int)(i / J), ch = (int)(i % J);
+            dg[(int64_t)t * a.dg_st + ch * a.dg_sj] += cp[(int64_t)(t / C) * (2 * J + 2) + ch];
+        }
+    }
+}
+
+// ---------------------------------------------------------------- 6. per-head parameters
+template <int D, int J, bool GENERAL>
+__global__ __launch_bounds__(256) void gla_bwd_param_kernel(GlaBwdK a) {
+    const int h = blockIdx.x, H = a.f.H, B = a.f.B, nc = a.f.nc;
+    for (int d = threadIdx.x; d < D; d += 256) {
+        float s = 0.f;
+        for (int b = 0; b < B; ++b)
+            for (int tile = 0; tile < a.ntile; ++tile) s += a.dgs_part[((int64_t)(b * H + h) * a.ntile + tile) * D + d];
+        store_any(a.dgs, a.dgs_dt, h * a.dgs_sh + d * a.dgs_sd, s);
+    }
+    if constexpr (!GENERAL) {
+        if (!a.dla) return;
+        for (int ch = threadIdx.x; ch < J; ch += 256) {
+            const float alpha = expf(load_any(a.f.la, a.f.la_dt, h * a.f.la_sh + ch * a.f.la_sj));
+            float s = 0.f;
+            for (int b = 0; b < B; ++b) {
+                const float *cp = a.chunk_part + (int64_t)(b * H + h) * nc * (2 * J + 2);
+                float lam = 0.f;  // cumsum of log_gamma before the chunk
+                for (int c = 0; c < nc; ++c) {
+                    const float *p = cp + (int64_t)c * (2 * J + 2);
+                    s += fmaf(lam, p[ch], p[J + ch]);
+                    lam += p[2 * J + 1];
+                }
+            }
+            store_any(a.dla, a.dla_dt, h * a.dla_sh + ch * a.dla_sj, alpha * s);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ host
+int elem_bytes(int dt) { return dt == HOFA_F32 ? 4 : 2; }
+
+bool rows_ok(const hofa_view_t &v, int es) {
+    return v.stride[3] == 1 && ((uintptr_t)v.data % 16) == 0 && (v.stride[0] * es) % 16 == 0 &&
+           (v.stride[1] * es) % 16 == 0 && (v.stride[2] * es) % 16 == 0;
+}
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+struct WsLayout {
+    size_t dO, dh, gl, dse, dlg, cp, dgs, total;
+};
+
+WsLayout ws_layout(const hofa_gla_bwd_args_t *a) {
+    const size_t bh = (size_t)a->B * a->H, T = a->T, D = a->D, J = a->D - a->R;
+    const size_t nc = (T + C - 1) / C, ntile = (T + ET - 1) / ET;
+    WsLayout w{};
+    w.dO = 0;
+    w.dh = w.dO + align256(bh * T * D * elem_bytes(a->q.dtype));
+    w.gl = w.dh + align256(bh * nc * D * J * 4);
+    w.dse = w.gl + align256(bh * nc * J * 4);
+    w.dlg = w.dse + align256(bh * nc * 4 * D * J * 2);
+    w.cp = w.dlg + align256(bh * T * 4);
+    w.dgs = w.cp + align256(bh * nc * (2 * J + 2) * 4);
+    w.total = w.dgs + align256(bh * ntile * D * 4);
+    return w;
+}
+
+int validate(const hofa_gla_bwd_args_t *a) {
+    HOFA_REQUIRE(a, HOFA_EINVAL, "hofa_gla_bwd: args is NULL");
+    HOFA_REQUIRE(a->B > 0 && a->H > 0 && a->T > 0, HOFA_EINVAL, "hofa_gla_bwd: B=%d H=%d T=%d must be positive", a->B,
+                 a->H, a->T);
+    HOFA_REQUIRE(a->T <= C * kMaxChunks, HOFA_EUNSUPPORTED, "hofa_gla_bwd: T=%d exceeds %d", a->T, C * kMaxChunks);
+    HOFA_REQUIRE(a->D == 64 || a->D == 128, HOFA_EUNSUPPORTED, "hofa_gla_bwd: head dim D=%d not in {64,128}", a->D);
+    const int J = a->D - a->R;
+    HOFA_REQUIRE(a->R >= 0 && J >= 16 && J % 16 == 0, HOFA_EUNSUPPORTED,
+                 "hofa_gla_bwd: inlier width J=%d must be a positive multiple of 16", J);
+    const int dt = a->q.dtype;
+    HOFA_REQUIRE(dt == HOFA_F32 || dt == HOFA_BF16 || dt == HOFA_F16, HOFA_EINVAL, "hofa_gla_bwd: bad dtype %d", dt);
+    const int es = elem_bytes(dt);
+    for (const hofa_view_t *v : {&a->q, &a->k, &a->v, &a->n, &a->dy, &a->dq, &a->dk, &a->dv}) {
+        HOFA_REQUIRE(v->data, HOFA_EINVAL, "hofa_gla_bwd: NULL tensor pointer");
+        HOFA_REQUIRE(v->dtype == dt, HOFA_EINVAL, "hofa_gla_bwd: q, k, v, n, dy, dq, dk, dv must share one dtype");
+        HOFA_REQUIRE(rows_ok(*v, es), HOFA_EINVAL, "hofa_gla_bwd: tensors need unit last stride and 16-byte aligned rows");
+    }
+    for (const hofa_view_t *v : {&a->o, &a->dout_attn}) {
+        if (!v->data) continue;
+        HOFA_REQUIRE(v->dtype == dt && rows_ok(*v, es), HOFA_EINVAL,
+                     "hofa_gla_bwd: o and dout_attn need the dtype of q and aligned rows");
+    }
+    HOFA_REQUIRE((a->R * es) % 16 == 0, HOFA_EINVAL, "hofa_gla_bwd: the inlier columns must start 16-byte aligned");
+    HOFA_REQUIRE(a->rstd && a->chunk_states && ((uintptr_t)a->chunk_states % 16) == 0, HOFA_EINVAL,
+                 "hofa_gla_bwd: rstd and 16-byte aligned chunk_states from the forward are required");
+    HOFA_REQUIRE(a->gla_scale.data && a->d_gla_scale.data, HOFA_EINVAL, "hofa_gla_bwd: gla_scale and d_gla_scale are required");
+    if (a->g.data) {
+        HOFA_REQUIRE(a->g.dtype == HOFA_F32 && a->d_g.data && a->d_g.dtype == HOFA_F32, HOFA_EINVAL,
+                     "hofa_gla_bwd: general decay needs float32 g and d_g");
+    } else {
+        HOFA_REQUIRE(a->log_gamma.data && a->d_log_gamma.data, HOFA_EINVAL,
+                     "hofa_gla_bwd: give log_gamma and d_log_gamma (or g and d_g)");
+    }
+    HOFA_REQUIRE(!a->d_log_alpha.data || (a->log_alpha.data && !a->g.data), HOFA_EINVAL,
+                 "hofa_gla_bwd: d_log_alpha needs log_alpha and scalar decay");
+    HOFA_REQUIRE(!a->d_mix.data || a->mix.data, HOFA_EINVAL, "hofa_gla_bwd: d_mix needs mix");
+    HOFA_REQUIRE(!a->delta || a->o.data, HOFA_EINVAL, "hofa_gla_bwd: delta needs o");
+    return HOFA_OK;
+}
+
+template <int DT, int D, int J, bool GEN>
+void launch(const GlaBwdK &k, hipStream_t s) {
+    const int nbh = k.f.B * k.f.H;
+    hipLaunchKernelGGL((gla_bwd_epilogue_kernel<DT, D>), dim3(nbh, k.ntile), dim3(256), 0, s, k);
+    GlaK fk = k.f;  // dH^T = dO^T (q e^G): key operand q at column R, value operand dO
+    fk.k = k.f.q;
+    fk.k_sb = k.f.q_sb; fk.k_sh = k.f.q_sh; fk.k_st = k.f.q_st;
+    fk.key_col0 = k.f.R;
+    fk.v = k.ws_do;
+    fk.v_sb = (int64_t)k.f.H * k.f.T * D; fk.v_sh = (int64_t)k.f.T * D; fk.v_st = D;
+    fk.ws_ds = k.ws_dh;
+    fk.ws_gl = k.ws_gl;
+    hipLaunchKernelGGL((gla_state_kernel<DT, D, J, GEN, true>), dim3(nbh * k.f.nc), dim3(kStateThreads), 0, s, fk);
+    hipLaunchKernelGGL((gla_bwd_scan_kernel<DT, D, J>), dim3(nbh, (D * J / 4 + 255) / 256), dim3(256), 0, s, k);
+    hipLaunchKernelGGL((gla_bwd_chunk_kernel<DT, D, J, GEN>), dim3(nbh * k.f.nc), dim3(NTB), 0, s, k);
+    hipLaunchKernelGGL((gla_bwd_dlg_kernel<J, GEN>), dim3(nbh), dim3(256), 0, s, k);
+    hipLaunchKernelGGL((gla_bwd_param_kernel<D, J, GEN>), dim3(k.f.H), dim3(256), 0, s, k);
+}
+
+template <int DT, bool GEN>
+int dispatch(const GlaBwdK &k, int D, int J, hipStream_t s) {
+    if (D == 64 && J == 48) launch<DT, 64, 48, GEN>(k, s);
+    else if (D == 64 && J == 32) launch<DT, 64, 32, GEN>(k, s);
+    else if (D == 64 && J == 64) launch<DT, 64, 64, GEN>(k, s);
+    else if (D == 128 && J == 112) launch<DT, 128, 112, GEN>(k, s);
+    else if (D == 128 && J == 96) launch<DT, 128, 96, GEN>(k, s);
+    else if (D == 128 && J == 64) launch<DT, 128, 64, GEN>(k, s);
+    else if (D == 128 && J == 128) launch<DT, 128, 128, GEN>(k, s);
+    else return HOFA_EUNSUPPORTED;
+    return HOFA_OK;
+}
+
+}  // namespace
+}  // namespace hofa
+
+using namespace hofa;
+
+extern "C" size_t hofa_gla_bwd_workspace_bytes(const hofa_gla_bwd_args_t *a) {
+    if (validate(a)) return 0;
+    return ws_layout(a).total;
+}
+
+extern "C" int hofa_gla_bwd(const hofa_gla_bwd_args_t *a, void *workspace, size_t workspace_bytes, void *stream) {
+    int rc = validate(a);
+    if (rc) return rc;
+    const WsLayout L = ws_layout(a);
+    HOFA_REQUIRE(workspace && workspace_bytes >= L.total, HOFA_EWORKSPACE,
+                 "hofa_gla_bwd: workspace of %zu bytes needed, got %zu", L.total, workspace_bytes);
+    HOFA_REQUIRE(((uintptr_t)workspace % 256) == 0, HOFA_EWORKSPACE, "hofa_gla_bwd: workspace must be 256-byte aligned");
+    GlaBwdK k{};
+    GlaK &f = k.f;
+    f.q = a->q.data; f.k = a->k.data; f.v = a->v.data;
+    f.lg = a->log_gamma.data; f.la = a->log_alpha.data; f.g = a->g.data;
+    f.mix = a->mix.data; f.gs = a->gla_scale.data;
+    f.q_sb = a->q.stride[0]; f.q_sh = a->q.stride[1]; f.q_st = a->q.stride[2];
+    f.k_sb = a->k.stride[0]; f.k_sh = a->k.stride[1]; f.k_st = a->k.stride[2];
+    f.v_sb = a->v.stride[0]; f.v_sh = a->v.stride[1]; f.v_st = a->v.stride[2];
+    f.lg_sb = a->log_gamma.stride[0]; f.lg_sh = a->log_gamma.stride[1]; f.lg_st = a->log_gamma.stride[2];
+    f.la_sh = a->log_alpha.stride[0]; f.la_sj = a->log_alpha.stride[1];
+    f.g_sb = a->g.stride[0]; f.g_sh = a->g.stride[1]; f.g_st = a->g.stride[2]; f.g_sj = a->g.stride[3];
+    f.m_sb = a->mix.stride[0]; f.m_sh = a->mix.stride[1]; f.m_st = a->mix.stride[2];
+    f.gs_sh = a->gla_scale.stride[0]; f.gs_sd = a->gla_scale.stride[1];
+    f.lg_dt = a->log_gamma.dtype; f.la_dt = a->log_alpha.dtype; f.mix_dt = a->mix.dtype; f.gs_dt = a->gla_scale.dtype;
+    f.B = a->B; f.H = a->H; f.T = a->T; f.R = a->R;
+    f.nc = (a->T + C - 1) / C;
+    k.dy = a->dy.data; k.n = a->n.data; k.o = a->o.data;
+    k.rstd = a->rstd;
+    k.s_in = (const uint16_t *)a->chunk_states;
+    k.dq = (void *)a->dq.data; k.dk = (void *)a->dk.data; k.dv = (void *)a->dv.data;
+    k.dlg = (void *)a->d_log_gamma.data; k.dg = (void *)a->d_g.data; k.dla = (void *)a->d_log_alpha.data;
+    k.dmix = (void *)a->d_mix.data; k.dgs = (void *)a->d_gla_scale.data; k.dout = (void *)a->dout_attn.data;
+    k.delta = a->delta;
+    k.dy_sb = a->dy.stride[0]; k.dy_sh = a->dy.stride[1]; k.dy_st = a->dy.stride[2];
+    k.n_sb = a->n.stride[0]; k.n_sh = a->n.stride[1]; k.n_st = a->n.stride[2];
+    k.o_sb = a->o.stride[0]; k.o_sh = a->o.stride[1]; k.o_st = a->o.stride[2];
+    k.dq_sb = a->dq.stride[0]; k.dq_sh = a->dq.stride[1]; k.dq_st = a->dq.stride[2];
+    k.dk_sb = a->dk.stride[0]; k.dk_sh = a->dk.stride[1]; k.dk_st = a->dk.stride[2];
+    k.dv_sb = a->dv.stride[0]; k.dv_sh = a->dv.stride[1]; k.dv_st = a->dv.stride[2];
+    k.dlg_sb = a->d_log_gamma.stride[0]; k.dlg_sh = a->d_log_gamma.stride[1]; k.dlg_st = a->d_log_gamma.stride[2];
+    k.dg_sb = a->d_g.stride[0]; k.dg_sh = a->d_g.stride[1]; k.dg_st = a->d_g.stride[2]; k.dg_sj = a->d_g.stride[3];
+    k.dla_sh = a->d_log_alpha.stride[0]; k.dla_sj = a->d_log_alpha.stride[1];
+    k.dmix_sb = a->d_mix.stride[0]; k.dmix_sh = a->d_mix.stride[1]; k.dmix_st = a->d_mix.stride[2];
+    k.dgs_sh = a->d_gla_scale.stride[0]; k.dgs_sd = a->d_gla_scale.stride[1];
+    k.do_sb = a->dout_attn.stride[0]; k.do_sh = a->dout_attn.stride[1]; k.do_st = a->dout_attn.stride[2];
+    k.dlg_dt = a->d_log_gamma.dtype; k.dla_dt = a->d_log_alpha.dtype; k.dmix_dt = a->d_mix.dtype;
+    k.dgs_dt = a->d_gla_scale.dtype;
+    char *w = (char *)workspace;
+    k.ws_do = w + L.dO;
+    k.ws_dh = (float *)(w + L.dh);
+    k.ws_gl = (float *)(w + L.gl);
+    k.ds_end = (uint16_t *)(w + L.dse);
+    k.dlg_part = (float *)(w + L.dlg);
+    k.chunk_part = (float *)(w + L.cp);
+    k.dgs_part = (float *)(w + L.dgs);
+    k.ntile = (a->T + ET - 1) / ET;
+    const int J = a->D - a->R;
+    hipStream_t s = (hipStream_t)stream;
+    const bool gen = a->g.data != nullptr;
+    switch (a->q.dtype) {
+        case HOFA_F32: rc = gen ? dispatch<HOFA_F32, true>(k, a->D, J, s) : dispatch<HOFA_F32, false>(k, a->D, J, s); break;
+        case HOFA_BF16: rc = gen ? dispatch<HOFA_BF16, true>(k, a->D, J, s) : dispatch<HOFA_BF16, false>(k, a->D, J, s); break;
+        default: rc = gen ? dispatch<HOFA_F16, true>(k, a->D, J, s) : dispatch<HOFA_F16, false>(k, a->D, J, s); break;
+    }
+    if (rc) {
+        set_error("hofa_gla_bwd: no kernel for this (D, J)");
+        return rc;
+    }
+    return check_launch("hofa_gla_bwd");
+}

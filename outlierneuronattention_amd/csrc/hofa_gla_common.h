@@ -1,0 +1,232 @@
+// Pieces shared by the chunked GLA forward (hofa_gla.hip) and backward
+// (hofa_gla_bwd.hip): chunk constants, the in-chunk decay cumsum, transposed
+// LDS staging, and the per-chunk outer-product kernel used by both passes
+// (forward: dS^T = V^T (K (.) exp(G_last - G)); backward: dH^T = dO^T (Q (.) exp(G))).
+#pragma once
+
+#include "hofa_mfma.h"
+
+namespace hofa {
+namespace gla {
+
+constexpr int C = 64;               // chunk length
+constexpr float kSafeRange = 64.f;  // max in-chunk -G for factored exp(+-G) operands (exp(64) ~ 6e27)
+
+// Every GLA matrix product takes bf16 operands (the f32 exponent range keeps
+// the factored exp(+-G) operands finite); f32 and f16 inputs are split into a
+// bf16 hi/lo pair (exact for f16), bf16 inputs are used as they are.
+constexpr int OPB = HOFA_BF16;
+template <int DT> constexpr bool kRawSplit = DT != HOFA_BF16;
+
+// 8 consecutive input elements -> bf16 operand hi and the rounding remainder lo
+// (lo is zero for bf16 inputs).
+template <int DT>
+__device__ __forceinline__ void raw_op8(const typename Stor<DT>::type *p, u32x4 &hi, u32x4 &lo) {
+    if constexpr (DT == HOFA_BF16) {
+        hi = *(const u32x4 *)p;
+        lo = u32x4{0, 0, 0, 0};
+    } else {
+        float x[8];
+        if constexpr (DT == HOFA_F32) {
+            const f32x4 u = *(const f32x4 *)p, w = *(const f32x4 *)(p + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[e] = u[e];
+                x[4 + e] = w[e];
+            }
+        } else {
+            unpack16<DT>(*(const u32x4 *)p, x);
+        }
+        split8<OPB>(x, hi, lo);
+    }
+}
+
+// Where a chunk kernel finds its inputs.  Forward and backward fill the
+// fields they use; strides are in elements.
+struct GlaK {
+    const void *q, *k, *v, *lg, *la, *g, *mix, *gs;
+    void *y;
+    void *n_out;        // optional RMSNorm(Y_I) before the gate (forward)
+    float *rstd;        // optional 1/sqrt(mean(Y_I^2)+eps) per token (forward)
+    float *state_out;
+    float *ws_ds;       // [B*H][nc][D][J] f32 per-chunk outer products
+    float *ws_gl;       // [B*H][nc][J] f32 per-chunk total log decay
+    uint16_t *s_in;     // [B*H][nc][nplanes][D*J] entering states as 16-bit hi/lo planes
+    int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, y_sb, y_sh, y_st;
+    int64_t n_sb, n_sh, n_st;
+    int64_t lg_sb, lg_sh, lg_st, la_sh, la_sj, g_sb, g_sh, g_st, g_sj;
+    int64_t m_sb, m_sh, m_st, gs_sh, gs_sd;
+    int64_t so_sb, so_sh, so_sj, so_sd;
+    int lg_dt, la_dt, mix_dt, gs_dt;
+    int B, H, T, R, nc;
+    int key_col0;       // first column of the key operand of gla_state_kernel
+    int nplanes;        // 2: hi/lo of S^T [D][J]; 4: also hi/lo of S [J][D]
+    int fuse;
+    float eps;
+};
+
+// In-chunk inclusive cumsum of the log decay into sG[C][J] (tokens past T
+// decay by 0).  Scalar decay also leaves the cumsum of log_gamma in
+// sAux[0..C) and exp(log_alpha) in sAux[C..C+J).
+template <int J, bool GENERAL, int NTH>
+__device__ void chunk_cumsum(const GlaK &a, int b, int h, int t0, float *sG, float *sAux) {
+    const int tid = threadIdx.x;
+    if constexpr (!GENERAL) {
+        float *sLam = sAux, *sAl = sAux + C;
+        if (tid < 64) {
+            const int t = t0 + tid;
+            float x = t < a.T ? load_any(a.lg, a.lg_dt, b * a.lg_sb + h * a.lg_sh + (int64_t)t * a.lg_st) : 0.f;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float y = __shfl_up(x, off);
+                if (tid >= off) x += y;
+            }
+            sLam[tid] = x;
+        }
+        for (int c = tid; c < J; c += NTH) sAl[c] = a.la ? expf(load_any(a.la, a.la_dt, h * a.la_sh + c * a.la_sj)) : 1.f;
+        __syncthreads();
+        for (int idx = tid; idx < C * J; idx += NTH) sG[idx] = sLam[idx / J] * sAl[idx % J];
+    } else {
+        const float *gp = (const float *)a.g + b * a.g_sb + h * a.g_sh;
+        for (int c = tid; c < J; c += NTH) {
+            float acc = 0.f;
+#pragma unroll 8
+            for (int t = 0; t < C; ++t) {
+                const int tt = t0 + t;
+                acc += tt < a.T ? gp[(int64_t)tt * a.g_st + c * a.g_sj] : 0.f;
+                sG[t * J + c] = acc;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Copy one chunk of rows [t0, t0+C) x columns [col0, col0+W) into LDS
+// transposed ([W][pitch] bf16 operands), scaled per element; with LO the
+// rounding remainder goes to dst_lo.  Rows past T are zero.
+template <int DT, int W, int PITCH, bool LO, int NTH, typename Scale>
+__device__ void load_transposed(const typename Stor<DT>::type *base, int64_t row_stride, int col0, int t0, int T,
+                                uint16_t *dst, uint16_t *dst_lo, Scale scale) {
+    using in_t = typename Stor<DT>::type;
+    constexpr int NPIECE = (C / 2) * (W / 8);
+    for (int pi = threadIdx.x; pi < NPIECE; pi += NTH) {
+        const int tp = pi / (W / 8), cc = pi % (W / 8);
+        const int t = 2 * tp;
+        float x[2][8];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int tt = t0 + t + r;
+            if (tt < T) {
+                const in_t *p = base + (int64_t)tt * row_stride + col0 + 8 * cc;
+                if constexpr (DT == HOFA_F32) {
+                    const f32x4 u = *(const f32x4 *)p, w = *(const f32x4 *)(p + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        x[r][e] = u[e];
+                        x[r][4 + e] = w[e];
+                    }
+                } else {
+                    unpack16<DT>(*(const u32x4 *)p, x[r]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[r][e] = 0.f;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[r][e] *= scale(t + r, 8 * cc + e);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t hv = pack2<OPB>(x[0][e], x[1][e]);
+            *(uint32_t *)&dst[(8 * cc + e) * PITCH + t] = hv;
+            if constexpr (LO)
+                *(uint32_t *)&dst_lo[(8 * cc + e) * PITCH + t] =
+                    pack2<OPB>(x[0][e] - op_to_f32<OPB>(hv & 0xffffu), x[1][e] - op_to_f32<OPB>(hv >> 16));
+        }
+    }
+}
+
+constexpr int kStateThreads = 128;
+
+// Per chunk: in-chunk cumsum G of the log decay, then
+//   forward (BWD=false): out^T[D x J] = V_c^T (K_c (.) exp(G_last - G))
+//   backward (BWD=true): out^T[D x J] = dO_c^T (Q_c (.) exp(G))
+// with the key operand read at columns [key_col0, key_col0+J) of a.k and the
+// value operand from a.v (every exponent <= 0).  Writes out^T to ws_ds and
+// G_last to ws_gl.  2 waves, v_mfma_f32_16x16x32 tiles, hi/lo split operands.
+template <int DT, int D, int J, bool GENERAL, bool BWD>
+__global__ __launch_bounds__(kStateThreads) void gla_state_kernel(GlaK a) {
+    using in_t = typename Stor<DT>::type;
+    constexpr int NTH = kStateThreads;
+    constexpr int TP = C + 8;               // token pitch of the transposed tiles
+    constexpr bool VLO = kRawSplit<DT>;     // f32/f16 inputs also split the value operand
+    __shared__ float sG[C * J];
+    __shared__ float sAux[C + J];
+    __shared__ __attribute__((aligned(16))) uint16_t sKt[2][J * TP];
+    __shared__ __attribute__((aligned(16))) uint16_t sVt[VLO ? 2 : 1][D * TP];
+    const int bh = blockIdx.x / a.nc, c = blockIdx.x % a.nc;
+    const int b = bh / a.H, h = bh % a.H, t0 = c * C;
+    chunk_cumsum<J, GENERAL, NTH>(a, b, h, t0, sG, sAux);
+    const float *gl = sG + (C - 1) * J;
+    const in_t *kb = (const in_t *)a.k + b * a.k_sb + h * a.k_sh;
+    if constexpr (BWD)
+        load_transposed<DT, J, TP, true, NTH>(kb, a.k_st, a.key_col0, t0, a.T, sKt[0], sKt[1],
+                                              [&](int t, int ch) { return fast_exp2(sG[t * J + ch] * kLog2e); });
+    else
+        load_transposed<DT, J, TP, true, NTH>(kb, a.k_st, a.key_col0, t0, a.T, sKt[0], sKt[1], [&](int t, int ch) {
+            return fast_exp2((gl[ch] - sG[t * J + ch]) * kLog2e);
+        });
+    load_transposed<DT, D, TP, VLO, NTH>((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, 0, t0, a.T, sVt[0],
+                                         sVt[VLO ? 1 : 0], [](int, int) { return 1.f; });
+    __syncthreads();
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int r16 = lane & 15, g4 = lane >> 4;
+    float *ds = a.ws_ds + ((int64_t)bh * a.nc + c) * D * J;
+    constexpr int NTILE = (D / 16) * (J / 16);
+    for (int tile = w; tile < NTILE; tile += NTH / 64) {
+        const int tm = tile / (J / 16), tn = tile % (J / 16);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < C / 32; ++ks) {
+            const int vo = (16 * tm + r16) * TP + 32 * ks + 8 * g4;
+            const int ko = (16 * tn + r16) * TP + 32 * ks + 8 * g4;
+            const u32x4 av = *(const u32x4 *)&sVt[0][vo];
+            acc = mfma16<OPB>(av, *(const u32x4 *)&sKt[0][ko], acc);
+            acc = mfma16<OPB>(av, *(const u32x4 *)&sKt[1][ko], acc);
+            if constexpr (VLO) acc = mfma16<OPB>(*(const u32x4 *)&sVt[VLO ? 1 : 0][vo], *(const u32x4 *)&sKt[0][ko], acc);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) ds[(16 * tm + 4 * g4 + v) * J + 16 * tn + r16] = acc[v];
+    }
+    for (int ch = threadIdx.x; ch < J; ch += NTH) a.ws_gl[((int64_t)bh * a.nc + c) * J + ch] = gl[ch];
+}
+
+// hi/lo 16-bit planes of 4 consecutive floats.
+__device__ __forceinline__ void split4(const f32x4 &s, uint2 &hv, uint2 &lv) {
+    hv = uint2{pack2<OPB>(s[0], s[1]), pack2<OPB>(s[2], s[3])};
+    lv = uint2{pack2<OPB>(s[0] - op_to_f32<OPB>(hv.x & 0xffffu), s[1] - op_to_f32<OPB>(hv.x >> 16)),
+               pack2<OPB>(s[2] - op_to_f32<OPB>(hv.y & 0xffffu), s[3] - op_to_f32<OPB>(hv.y >> 16))};
+}
+
+// Store the state elements (dv, j4..j4+3) of one chunk as bf16 hi/lo planes:
+// planes 0/1 hold S^T ([D][J], j contiguous); with four planes, planes 2/3
+// hold S ([J][D], d contiguous).
+template <int DT, int D, int J>
+__device__ __forceinline__ void store_state_planes(uint16_t *dst, int nplanes, int dv, int j4, const f32x4 &S) {
+    uint2 hv, lv;
+    split4(S, hv, lv);
+    *(uint2 *)(dst + dv * J + j4) = hv;
+    *(uint2 *)(dst + D * J + dv * J + j4) = lv;
+    if (nplanes == 4) {
+        uint16_t *p2 = dst + 2 * D * J, *p3 = dst + 3 * D * J;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t hb = e < 2 ? hv.x : hv.y, lb = e < 2 ? lv.x : lv.y;
+            p2[(j4 + e) * D + dv] = (uint16_t)((e & 1) ? hb >> 16 : hb & 0xffffu);
+            p3[(j4 + e) * D + dv] = (uint16_t)((e & 1) ? lb >> 16 : lb & 0xffffu);
+        }
+    }
+}
+
+}  // namespace gla
+}  // namespace hofa

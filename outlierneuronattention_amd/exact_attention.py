@@ -63,3 +63,40 @@ def exact_attention(q, k, v, r: int, sm_scale: float, mix_g: Optional[torch.Tens
 
 # Name used by the reference's callers.
 exact_attention_triton = exact_attention
+
+
+def exact_attention_bwd(q, k, v, dout, lse, delta, r: int, sm_scale: float, dq=None, dk=None, dv=None,
+                        dv_accumulate: bool = False):
+    """Gradients of ``O = softmax(q[..., :r] k[..., :r]^T * sm_scale + causal) v``
+    given ``dout`` (dL/dO), the base-2 ``lse`` written by :func:`exact_attention`
+    and ``delta = rowsum(dout * O)`` (float32, B*H*T).  Returns ``(dq, dk, dv)``
+    with ``dq``/``dk`` of width ``r`` (``[B,H,T,r]``); ``dv_accumulate`` adds
+    into a given ``dv``.  The reference has no kernel here: it trains through
+    autograd of torch SDPA (src/HybridOutlierFactorizedAttentionTrain.py:258-259).
+    """
+    _lib.require_gpu(q, k, v, dout, lse, delta, dq, dk, dv)
+    lib = _lib.load()
+    B, H, T, _ = q.shape
+    D = v.shape[-1]
+    r = int(r)
+    if k.shape[:3] != (B, H, T) or v.shape[:3] != (B, H, T) or tuple(dout.shape) != (B, H, T, D):
+        raise _lib.HofaError("q/k/v/dout shapes disagree")
+    for name, t in (("lse", lse), ("delta", delta)):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != B * H * T:
+            raise _lib.HofaError(f"{name} must be a contiguous float32 tensor of B*H*T elements")
+    if dq is None:
+        dq = torch.empty(B, H, T, r, dtype=q.dtype, device=q.device)
+    if dk is None:
+        dk = torch.empty(B, H, T, r, dtype=q.dtype, device=q.device)
+    if dv is None:
+        dv = torch.empty(B, H, T, D, dtype=v.dtype, device=v.device)
+        dv_accumulate = False
+    a = _lib.AttnBwdArgs()
+    a.B, a.H, a.T, a.D, a.R = B, H, T, D, r
+    a.sm_scale = float(sm_scale)
+    a.dv_accumulate = 1 if dv_accumulate else 0
+    a.q, a.k, a.v, a.dout = _lib.view(q), _lib.view(k), _lib.view(v), _lib.view(dout)
+    a.lse, a.delta = lse.data_ptr(), delta.data_ptr()
+    a.dq, a.dk, a.dv = _lib.view(dq), _lib.view(dk), _lib.view(dv)
+    _lib.check(lib.hofa_attn_bwd(ctypes.byref(a), _lib.stream_handle(q.device)), "exact_attention_bwd")
+    return dq, dk, dv
