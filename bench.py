@@ -1,6 +1,7 @@
 """HOFA hot-path benchmark on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 4] [--skip-cpu]
+                    [--only decode|prefill|train|copy] [--eager]
 
 A step is one pass of the hot path over one batch of synthetic input: one
 decode token of the BASELINE cfg3 workload (H=16, d_h=64, r=16, 32768-row bf16
@@ -69,7 +70,7 @@ def _decode_call(st):
                              st["mix"], st["nw"], R, L, math.sqrt(D / R))
 
 
-def bench_decode(B: int, steps: int, warmup: int, rotate_bytes: int = 1 << 30):
+def bench_decode(B: int, steps: int, warmup: int, rotate_bytes: int = 1 << 30, eager: bool = False):
     gen = torch.Generator().manual_seed(1234 + B)
     nbuf = max(1, math.ceil(rotate_bytes / decode_bytes(B)))
     sets = [make_decode_set(B, gen) for _ in range(nbuf)]
@@ -79,6 +80,16 @@ def bench_decode(B: int, steps: int, warmup: int, rotate_bytes: int = 1 << 30):
         for i in range(max(warmup, nbuf)):
             _decode_call(sets[i % nbuf])
         s.synchronize()
+        if eager:  # plain launches (for counter collection, which follows eager dispatches)
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record(s)
+            for i in range(steps):
+                _decode_call(sets[i % nbuf])
+            t1.record(s)
+            torch.cuda.synchronize()
+            step_s = t0.elapsed_time(t1) / 1e3 / steps
+            return dict(B=B, ms_per_step=step_s * 1e3, tok_per_s=B / step_s, bytes_per_step=decode_bytes(B),
+                        gbs=decode_bytes(B) / step_s / 1e9, rotation_sets=nbuf, timing="eager launches")
         full = torch.cuda.CUDAGraph()
         with torch.cuda.graph(full, stream=s):
             for st in sets:
@@ -301,6 +312,24 @@ def cpu_baseline_decode(B: int, budget_s: float = 10.0):
                        f"oracle/hofa_ref.decode_step, {el:.1f} s")
 
 
+def calibrate_copy(nbytes: int = 1 << 30, reps: int = 20):
+    """A plain device-to-device copy of known size: the reference point that
+    scales the FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize()
+    s = t0.elapsed_time(t1) / 1e3 / reps
+    return dict(bytes_read=nbytes, bytes_written=nbytes, us=round(s * 1e6, 2), gbs=round(2 * nbytes / s / 1e9, 1))
+
+
 def _traffic_from_profile(name: str):
     """HBM bytes per launch from a committed rocprofv3 PMC summary, if present."""
     path = os.path.join(ROOT, "profiles", name)
@@ -323,6 +352,9 @@ def main():
     ap.add_argument("--batch", type=int, default=4, help="batch of the headline decode line")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "train", "copy"], default="all",
+                    help="run one leg and print its result (profiling runs); default: the full line")
+    ap.add_argument("--eager", action="store_true", help="decode with plain launches instead of graph replay")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the multi-GPU "
@@ -331,6 +363,18 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+
+    if args.only != "all":
+        if args.only == "decode":
+            res = bench_decode(args.batch, args.steps, args.warmup, eager=args.eager)
+        elif args.only == "prefill":
+            res = bench_prefill(max(5, min(50, args.steps // 20)), 3)
+        elif args.only == "train":
+            res = bench_train(max(5, min(20, args.steps // 50)), 3)
+        else:
+            res = calibrate_copy()
+        print(json.dumps({"only": args.only, "result": res}), flush=True)
+        return
 
     other = 1 if args.batch != 1 else 4
     head = bench_decode(args.batch, args.steps, args.warmup)

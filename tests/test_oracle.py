@@ -201,3 +201,23 @@ def test_planted_mistakes_are_caught(mutation, monkeypatch):
                                     None if log_alpha is None else torch.log(log_alpha.abs() + 1e-3)))
     y, _, _ = _run_steps(m, g["x"])
     assert not torch.allclose(y.float(), g["y"], rtol=1e-3, atol=1e-3), mutation
+
+
+def test_core_backward_matches_finite_differences():
+    """The backward target of the GPU kernels is autograd of ``hofa_core``; pin
+    it against central finite differences (torch.autograd.gradcheck, float64)
+    on a tiny shape that spans two chunks, with per-channel decay and a mix."""
+    torch.manual_seed(11)
+    B, H, T, D, r = 1, 1, 6, 8, 2
+    J = D - r
+    q = torch.randn(B, H, T, D, dtype=torch.float64, requires_grad=True)
+    k = torch.randn(B, H, T, D, dtype=torch.float64, requires_grad=True)
+    v = torch.randn(B, H, T, D, dtype=torch.float64, requires_grad=True)
+    g = (torch.nn.functional.logsigmoid(torch.randn(B, H, T, J, dtype=torch.float64)) * 0.5).requires_grad_()
+    mix = torch.sigmoid(torch.randn(B, H, T, dtype=torch.float64)).requires_grad_()
+    gs = (1 + 0.3 * torch.randn(1, H, 1, D, dtype=torch.float64)).requires_grad_()
+
+    def f(q, k, v, g, mix, gs):
+        return ref.hofa_core(q, k, v, g, mix, gs, r, 1.3, eps=1e-6, chunk=4)[0]
+
+    assert torch.autograd.gradcheck(f, (q, k, v, g, mix, gs), eps=1e-6, atol=1e-7, rtol=1e-5)
