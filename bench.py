@@ -249,8 +249,8 @@ def make_train_inputs(gen, dev="cuda"):
 def _train_step(inp, dy, backward=True):
     from outlierneuronattention_amd.autograd import hofa_core
     q, k = inp["q"], inp["k"]
-    y = hofa_core(q[..., :T_R], k[..., :T_R], q, k, inp["v"], inp["lg"], inp["la"], inp["mix"], inp["gs"], T_R,
-                  math.sqrt(T_D / T_R))
+    y = hofa_core(None, None, q, k, inp["v"], inp["lg"], inp["la"], inp["mix"], inp["gs"], T_R,
+                  math.sqrt(T_D / T_R))  # outlier channels = q[..., :r], k[..., :r] (RoPE is outside the core)
     if backward:
         y.backward(dy)
     return y

@@ -125,10 +125,10 @@ class HybridOutlierFactorizedAttention(nn.Module):
         if self.r == 0:
             Y = hofa_core(None, None, Q, K, V, log_gamma, log_alpha, None, self.gla_scale, 0, 1.0)
             return self._merge(Y)
-        Q_O, K_O = Q[..., :self.r], K[..., :self.r]
+        Q_O = K_O = None  # without RoPE the outlier channels are Q[..., :r], K[..., :r] in place
         if getattr(self, "rotary_emb", None) is not None:
             cos, sin = self.rotary_emb(N)
-            Q_O, K_O = apply_rotary_pos_emb(Q_O, K_O, cos, sin)
+            Q_O, K_O = apply_rotary_pos_emb(Q[..., :self.r], K[..., :self.r], cos, sin)
         sm_scale = ((self.d_head / self.r) ** 0.5) * self.attention_scale
         Y = hofa_core(Q_O, K_O, Q, K, V, log_gamma, log_alpha, mix_g.squeeze(-1), self.gla_scale, self.r, sm_scale)
         return self._merge(Y)

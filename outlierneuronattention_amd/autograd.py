@@ -11,8 +11,10 @@ with RMSNorm eps = finfo(float32).eps.  This is the Train module's hybrid
 forward after projections, gates and RoPE (SDPA + fla ``chunk_gla`` +
 ``RMSNorm * gla_scale`` + ``lerp``, src/HybridOutlierFactorizedAttentionTrain.py:233-294).
 ``q_o``/``k_o`` are the RoPE'd outlier channels, ``q``/``k`` the projections
-whose channels ``[r, d_head)`` feed the GLA.  With ``r == 0`` (and no mix) it
-is the pure-GLA branch ``gla_scale * RMSNorm(GLA)`` (:201-223).
+whose channels ``[r, d_head)`` feed the GLA; ``q_o = k_o = None`` means the
+outlier channels are ``q[..., :r]`` / ``k[..., :r]`` themselves (no RoPE), and
+their gradients land in ``dq[..., :r]`` / ``dk[..., :r]`` directly.  With
+``r == 0`` (and no mix) it is the pure-GLA branch ``gla_scale * RMSNorm(GLA)`` (:201-223).
 
 The backward runs the HIP kernel pair ``hofa_gla_bwd`` (epilogue + inlier
 GLA) then ``hofa_attn_bwd`` (outlier softmax attention, accumulating into
@@ -63,7 +65,8 @@ class _HOFACore(torch.autograd.Function):
             if train and mix is not None:
                 o = torch.empty(B, H, T, D, dtype=v.dtype, device=dev)
                 lse = torch.empty(B * H * T, dtype=torch.float32, device=dev)
-            exact_attention(q_o, k_o, v, r, sm_scale, mix_eff, out=y, o=o, lse=lse)
+            exact_attention(q if q_o is None else q_o, k if k_o is None else k_o, v, r, sm_scale, mix_eff, out=y,
+                            o=o, lse=lse)
         if train:
             ctx.save_for_backward(q_o, k_o, q, k, v, log_gamma, log_alpha, mix, gla_scale, n, rstd, cs, o, lse)
             ctx.r, ctx.sm_scale = r, sm_scale
@@ -78,15 +81,21 @@ class _HOFACore(torch.autograd.Function):
         g = chunk_gla_inlier_bwd(q, k, v, log_gamma, r, dy, n, rstd, cs, gla_scale, log_alpha=log_alpha, mix_g=mix,
                                  o=o, want_attn_grad=attn)
         dq, dk, dv = g["dq"], g["dk"], g["dv"]
-        if r > 0:
-            dq[..., :r].zero_()
-            dk[..., :r].zero_()
+        shared = q_o is None  # outlier channels are q[..., :r]: their gradient goes into dq[..., :r]
         dq_o = dk_o = None
         if attn:
-            dq_o, dk_o, _ = exact_attention_bwd(q_o, k_o, v, g["dout_attn"], lse, g["delta"], r, sm_scale,
-                                                dv=dv, dv_accumulate=True)
-        elif r > 0:
-            dq_o, dk_o = torch.zeros_like(q_o), torch.zeros_like(k_o)
+            if shared:
+                exact_attention_bwd(q, k, v, g["dout_attn"], lse, g["delta"], r, sm_scale, dq=dq, dk=dk, dv=dv,
+                                    dv_accumulate=True)
+            else:
+                dq_o, dk_o, _ = exact_attention_bwd(q_o, k_o, v, g["dout_attn"], lse, g["delta"], r, sm_scale,
+                                                    dv=dv, dv_accumulate=True)
+        if r > 0 and not (attn and shared):
+            dq[..., :r].zero_()
+            dk[..., :r].zero_()
+            if not shared:
+                dq_o = dq_o if dq_o is not None else torch.zeros_like(q_o)
+                dk_o = dk_o if dk_o is not None else torch.zeros_like(k_o)
         d_lg = _grad_like(g["d_log_gamma"], log_gamma)
         d_la = _grad_like(g["d_log_alpha"], log_alpha) if log_alpha is not None else None
         d_mix = _grad_like(g["d_mix"], mix) if mix is not None else None

@@ -11,9 +11,15 @@
 //                                           tile sit in its registers and in lane l^32
 //   O^T[dv, query] += V_tile^T P^T          A = V^T from LDS (stored transposed), B = P straight
 //                                           from the score registers (keys permuted consistently)
-// so the row max, the row sum and the rescale of O never leave a lane pair.
-// K (row-major) and V^T tiles are double-buffered in LDS; the next tile's
-// global loads are in flight while the current tile is consumed.
+//   l[query] += 1^T P^T                     the row sum on the matrix core (A = ones), over the
+//                                           same rounded P that enters O (f32 inputs: an exact f32
+//                                           sum of the unrounded P)
+// so the row max and the rescale of O never leave a lane pair.  The rescale
+// is lazy: the reference max moves only when a tile's max exceeds it by more
+// than kTau (log2 units), so P stays below 2^kTau and O is rarely rescaled.
+// K (row-major) and V^T tiles are double-buffered in LDS and staged through
+// two register slots, so a tile's global loads have two tile-iterations to
+// arrive before they are written to LDS.
 #include "hofa_mfma.h"
 
 namespace hofa {
@@ -77,38 +83,39 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnFwdK a) {
     const int kend = min(a.T, q0 + BM);
     const int ntiles = (kend + BN - 1) / BN;
 
-    // ---- cooperative tile loader (registers -> LDS)
-    u32x4 kreg[NKC], klo[NKC];
-    u32x4 vreg[NVP][2];
-    auto gload = [&](int kt) {
+    // ---- cooperative tile loader (global -> registers -> LDS), two register
+    // slots so a tile's loads have two tile-iterations to arrive
+    u32x4 kreg[2][NKC], klo[2][NKC];
+    u32x4 vreg[2][NVP][2];
+    auto gload = [&](int kt, int sl) {
         const int k0 = kt * BN;
 #pragma unroll
         for (int i = 0; i < NKC; ++i) {
             const int ci = tid + NT * i;
             const int row = ci / (R / 8), part = ci % (R / 8);
             const int key = k0 + row;
-            kreg[i] = (ci < KCH && key < a.T) ? load_op8<DT>(kp + (int64_t)key * a.k_st + 8 * part) : u32x4{0, 0, 0, 0};
+            kreg[sl][i] = (ci < KCH && key < a.T) ? load_op8<DT>(kp + (int64_t)key * a.k_st + 8 * part) : u32x4{0, 0, 0, 0};
             if constexpr (SPLIT)
-                klo[i] = (ci < KCH && key < a.T) ? load_lo8_f32((const float *)kp + (int64_t)key * a.k_st + 8 * part)
-                                                 : u32x4{0, 0, 0, 0};
+                klo[sl][i] = (ci < KCH && key < a.T) ? load_lo8_f32((const float *)kp + (int64_t)key * a.k_st + 8 * part)
+                                                     : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int i = 0; i < NVP; ++i) {
             const int pi = tid + NT * i;
             const int kpair = pi / (D / 8), cch = pi % (D / 8);
             const int key = k0 + 2 * kpair;
-            vreg[i][0] = key < a.T ? load_op8<DT>(vp + (int64_t)key * a.v_st + 8 * cch) : u32x4{0, 0, 0, 0};
-            vreg[i][1] = key + 1 < a.T ? load_op8<DT>(vp + (int64_t)(key + 1) * a.v_st + 8 * cch) : u32x4{0, 0, 0, 0};
+            vreg[sl][i][0] = key < a.T ? load_op8<DT>(vp + (int64_t)key * a.v_st + 8 * cch) : u32x4{0, 0, 0, 0};
+            vreg[sl][i][1] = key + 1 < a.T ? load_op8<DT>(vp + (int64_t)(key + 1) * a.v_st + 8 * cch) : u32x4{0, 0, 0, 0};
         }
     };
-    auto lstore = [&](int buf) {
+    auto lstore = [&](int buf, int sl) {
 #pragma unroll
         for (int i = 0; i < NKC; ++i) {
             const int ci = tid + NT * i;
             if (ci < KCH) {
                 const int row = ci / (R / 8), part = ci % (R / 8);
-                *(u32x4 *)&sK[buf][row * KP + 8 * part] = kreg[i];
-                if constexpr (SPLIT) *(u32x4 *)&sK[buf][KLO + row * KP + 8 * part] = klo[i];
+                *(u32x4 *)&sK[buf][row * KP + 8 * part] = kreg[sl][i];
+                if constexpr (SPLIT) *(u32x4 *)&sK[buf][KLO + row * KP + 8 * part] = klo[sl][i];
             }
         }
 #pragma unroll
@@ -118,93 +125,118 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnFwdK a) {
             // transpose a (2 keys x 8 dv) piece: dv row gets the key pair as one dword
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const uint32_t x0 = vreg[i][0][e], x1 = vreg[i][1][e];
-                *(uint32_t *)&sV[buf][(8 * cch + 2 * e) * VP + 2 * kpair] = (x0 & 0xffffu) | (x1 << 16);
-                *(uint32_t *)&sV[buf][(8 * cch + 2 * e + 1) * VP + 2 * kpair] = (x0 >> 16) | (x1 & 0xffff0000u);
+                const uint32_t x0 = vreg[sl][i][0][e], x1 = vreg[sl][i][1][e];
+                *(uint32_t *)&sV[buf][(8 * cch + 2 * e) * VP + 2 * kpair] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+                *(uint32_t *)&sV[buf][(8 * cch + 2 * e + 1) * VP + 2 * kpair] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
             }
         }
     };
 
-    float m = -INFINITY, l = 0.f;
-    f32x16 o[MB];
+    constexpr float kTau = 8.f;
+    constexpr uint32_t kOne2 = kF16Ops<DT> ? 0x3C003C00u : 0x3F803F80u;  // two 16-bit 1.0
+    const u32x4 ones = {kOne2, kOne2, kOne2, kOne2};
+    float mref = -INFINITY;  // reference max of the scaled logits (base 2)
+    f32x16 o[MB], lacc;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[mb][v] = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) lacc[v] = 0.f;
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < ntiles; ++kt) {
-        const int buf = kt & 1;
-        const bool more = kt + 1 < ntiles;
-        if (more) gload(kt + 1);
+    float lsum = 0.f;  // f32 inputs: exact row sum of the unrounded probabilities
+    auto tile = [&](int kt, int buf) {
         const int k0 = kt * BN;
-        if (k0 <= qw0 + 31) {  // some key of this tile is visible to this wave
-            f32x16 s[2];
+        if (k0 > qw0 + 31) return;  // every key of this tile is after this wave's queries
+        f32x16 s[2];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int v = 0; v < 16; ++v) s[kb][v] = 0.f;
+            for (int v = 0; v < 16; ++v) s[kb][v] = 0.f;
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    const u32x4 ka = *(const u32x4 *)&sK[buf][(32 * kb + (lane & 31)) * KP + 16 * ks + 8 * hi];
-                    s[kb] = mfma32<DT>(ka, qop[ks], s[kb]);
-                    if constexpr (SPLIT) {
-                        const u32x4 kl = *(const u32x4 *)&sK[buf][KLO + (32 * kb + (lane & 31)) * KP + 16 * ks + 8 * hi];
-                        s[kb] = mfma32<DT>(ka, qlo[ks], s[kb]);
-                        s[kb] = mfma32<DT>(kl, qop[ks], s[kb]);
-                    }
+            for (int ks = 0; ks < KS; ++ks) {
+                const u32x4 ka = *(const u32x4 *)&sK[buf][(32 * kb + (lane & 31)) * KP + 16 * ks + 8 * hi];
+                s[kb] = mfma32<DT>(ka, qop[ks], s[kb]);
+                if constexpr (SPLIT) {
+                    const u32x4 kl = *(const u32x4 *)&sK[buf][KLO + (32 * kb + (lane & 31)) * KP + 16 * ks + 8 * hi];
+                    s[kb] = mfma32<DT>(ka, qlo[ks], s[kb]);
+                    s[kb] = mfma32<DT>(kl, qop[ks], s[kb]);
                 }
             }
-            if (k0 + BN - 1 > qw0 || k0 + BN > a.T) {  // tile crosses the diagonal or the end
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const int key = k0 + 32 * kb + 8 * (v / 4) + 4 * hi + (v % 4);
-                        if (key > qrow || key >= a.T) s[kb][v] = -INFINITY;
-                    }
-            }
-            float mx = s[0][0];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mn = fmaxf(m, mx);
-            const float alpha = fast_exp2((m - mn) * a.c);
-            const float mc = mn * a.c;
-            float ps = 0.f;
+        }
+        if (k0 + BN - 1 > qw0 || k0 + BN > a.T) {  // tile crosses the diagonal or the end
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    s[kb][v] = fast_exp2(fmaf(s[kb][v], a.c, -mc));
-                    ps += s[kb][v];
+                    const int key = k0 + 32 * kb + 8 * (v / 4) + 4 * hi + (v % 4);
+                    if (key > qrow || key >= a.T) s[kb][v] = -INFINITY;
                 }
-            l = fmaf(l, alpha, ps);
-            m = mn;
+        }
+        float t8[8];  // max as a tree (short dependency chains)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            t8[i] = fmaxf(fmaxf(s[0][i], s[0][i + 8]), fmaxf(s[1][i], s[1][i + 8]));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t8[i] = fmaxf(t8[i], t8[i + 4]);
+        float mx = fmaxf(fmaxf(t8[0], t8[1]), fmaxf(t8[2], t8[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.c;
+        if (__ballot(mx > mref + kTau)) {  // some row's max moved far: rescale (wave-uniform branch)
+            const float mn = fmaxf(mref, mx);
+            const float alpha = fast_exp2(mref - mn);  // 0 on the first tile (mref = -inf)
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) o[mb] *= alpha;
+            if constexpr (SPLIT) lsum *= alpha;
+            else lacc *= alpha;
+            mref = mn;
+        }
 #pragma unroll
-            for (int ks4 = 0; ks4 < 4; ++ks4) {
-                const u32x4 pb = pack8<DT>(s[ks4 / 2], 8 * (ks4 % 2));
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-                    const uint16_t *vr = &sV[buf][(32 * mb + (lane & 31)) * VP + 16 * ks4 + 4 * hi];
-                    const uint2 lo = *(const uint2 *)vr, hi8 = *(const uint2 *)(vr + 8);
-                    const u32x4 va = {lo.x, lo.y, hi8.x, hi8.y};
-                    o[mb] = mfma32<DT>(va, pb, o[mb]);
-                }
+            for (int v = 0; v < 16; ++v) s[kb][v] = fast_exp2(fmaf(s[kb][v], a.c, -mref));
+        if constexpr (SPLIT) {
+            float ps[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) ps[v % 4] += s[kb][v];
+            lsum += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+        }
+#pragma unroll
+        for (int ks4 = 0; ks4 < 4; ++ks4) {
+            const u32x4 pb = pack8<DT>(s[ks4 / 2], 8 * (ks4 % 2));
+            if constexpr (!SPLIT) lacc = mfma32<DT>(ones, pb, lacc);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const uint16_t *vr = &sV[buf][(32 * mb + (lane & 31)) * VP + 16 * ks4 + 4 * hi];
+                const uint2 lo = *(const uint2 *)vr, hi8 = *(const uint2 *)(vr + 8);
+                const u32x4 va = {lo.x, lo.y, hi8.x, hi8.y};
+                o[mb] = mfma32<DT>(va, pb, o[mb]);
             }
         }
-        if (more) lstore(buf ^ 1);
+    };
+
+    // tiles in pairs so the register slots are static: tile kt lives in LDS
+    // buffer kt%2 and register slot kt%2
+    gload(0, 0);
+    lstore(0, 0);
+    if (ntiles > 1) gload(1, 1);
+    __syncthreads();
+    for (int kt = 0; kt < ntiles; kt += 2) {
+        if (kt + 2 < ntiles) gload(kt + 2, 0);
+        tile(kt, 0);
+        if (kt + 1 < ntiles) lstore(1, 1);
+        __syncthreads();
+        if (kt + 1 >= ntiles) break;
+        if (kt + 3 < ntiles) gload(kt + 3, 1);
+        tile(kt + 1, 1);
+        if (kt + 2 < ntiles) lstore(0, 0);
         __syncthreads();
     }
 
     // ---- epilogue: y (+)= mix * O, optional O and lse
-    l += __shfl_xor(l, 32);
+    // every row of the ones-product holds the query's sum; f32 inputs sum in f32
+    const float l = SPLIT ? lsum + __shfl_xor(lsum, 32) : lacc[0];
     if (qrow >= a.T) return;
     const float inv = 1.f / l;
     const float mixv = a.mix ? load_any(a.mix, a.mix_dt, b * a.m_sb + h * a.m_sh + (int64_t)qrow * a.m_st) : 1.f;
@@ -224,7 +256,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnFwdK a) {
                 if (orow) orow[dv + e] = from_f32<DT>(ov);
             }
         }
-    if (a.lse && hi == 0) a.lse[(int64_t)bh * a.T + qrow] = m * a.c + __log2f(l);
+    if (a.lse && hi == 0) a.lse[(int64_t)bh * a.T + qrow] = mref + __log2f(l);
 }
 
 template <int DT, int R, int D>

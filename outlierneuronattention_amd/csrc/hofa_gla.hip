@@ -7,7 +7,7 @@
 // sequential over chunks:
 //
 //   1. gla_state_kernel   grid (B*H*nc), 2 waves: per chunk, in-chunk
-//      inclusive cumsum G of the log decay (LDS, fp32), then
+//      inclusive cumsum G of the log decay (fp32, see Decay), then
 //        dS^T[D x J] = V_c^T (K_c (.) exp(G_last - G))        v_mfma_f32_16x16x32
 //      every exponent <= 0.  Writes dS^T and G_last.
 //   2. gla_scan_kernel    grid (B*H, D*J/1024): S_in(c) = S, S <- exp(G_last) S + dS,
@@ -18,9 +18,9 @@
 //        Y^T[dv, query]  = V_c^T A^T + S_in^T Q~^T                           v_mfma_f32_32x32x16
 //      each lane owns one query row, so the fused epilogue
 //      (1 - mix) * gla_scale * RMSNorm(Y) (src/chunk_gla_inlier.py:130-141)
-//      reduces over D inside a lane pair.  K~ grows like exp(-G); a chunk
-//      whose decay range exceeds kSafeRange computes A^T element-wise with
-//      differences G_q - G_k <= 0 instead.
+//      reduces over D inside a lane pair.  K~ grows like exp(-G); chunks
+//      whose decay range exceeds kSafeRange go to a second launch of the
+//      kernel that forms A^T element-wise from differences G_q - G_k <= 0.
 // Every matrix-core product takes its operands as hi + lo pairs of bf16
 // values (x ~ hi + lo, see split8), i.e. about 16 mantissa bits in the f32
 // exponent range: the result tracks an fp32 computation rather than one
@@ -41,12 +41,22 @@ __global__ __launch_bounds__(256) void gla_scan_kernel(GlaK a) {
     const int dv = idx / (J / 4), j4 = (idx % (J / 4)) * 4;
     f32x4 S = {0.f, 0.f, 0.f, 0.f};
     const int64_t base = (int64_t)bh * a.nc;
-    for (int c = 0; c < a.nc; ++c) {
-        const f32x4 ds = *(const f32x4 *)(a.ws_ds + (base + c) * D * J + dv * J + j4);
-        const f32x4 gl = *(const f32x4 *)(a.ws_gl + (base + c) * J + j4);
-        store_state_planes<DT, D, J>(a.s_in + (base + c) * a.nplanes * D * J, a.nplanes, dv, j4, S);
+    constexpr int PF = 4;  // chunks whose loads are in flight together
+    for (int c0 = 0; c0 < a.nc; c0 += PF) {
+        f32x4 ds[PF], gl[PF];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) S[e] = fmaf(fast_exp2(gl[e] * kLog2e), S[e], ds[e]);
+        for (int u = 0; u < PF; ++u) {
+            const int c = min(c0 + u, a.nc - 1);
+            ds[u] = *(const f32x4 *)(a.ws_ds + (base + c) * D * J + dv * J + j4);
+            gl[u] = *(const f32x4 *)(a.ws_gl + (base + c) * J + j4);
+        }
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            if (c0 + u >= a.nc) break;
+            store_state_planes<DT, D, J>(a.s_in + (base + c0 + u) * a.nplanes * D * J, a.nplanes, dv, j4, S);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) S[e] = fmaf(fast_exp2(gl[u][e] * kLog2e), S[e], ds[u][e]);
+        }
     }
     const int b = bh / a.H, h = bh % a.H;
     float *so = a.state_out + b * a.so_sb + h * a.so_sh;
@@ -54,19 +64,23 @@ __global__ __launch_bounds__(256) void gla_scan_kernel(GlaK a) {
     for (int e = 0; e < 4; ++e) so[(j4 + e) * a.so_sj + dv * a.so_sd] = S[e];
 }
 
-template <int DT, int D, int J, bool GENERAL>
+// FB = false handles the chunks whose decay range is within kSafeRange with
+// factored operands; FB = true handles the others element-wise.  Both are
+// launched over every chunk and leave at once for the chunks of the other.
+template <int DT, int D, int J, bool GENERAL, bool FB>
 __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
     using in_t = typename Stor<DT>::type;
     constexpr int VP = C + 4;
     constexpr int MB = D / 32;
     constexpr int KS = J / 16;
     constexpr bool VLO = kRawSplit<DT>;  // f32/f16 inputs also split V
-    __shared__ float sG[C * J];
-    __shared__ float sAux[C + J];
+    __shared__ float sDec[Decay<J, GENERAL>::kFloats];
     __shared__ __attribute__((aligned(16))) uint16_t sVt[VLO ? 2 : 1][D * VP];
+    if ((a.unsafe[blockIdx.x] != 0) != FB) return;  // the other launch handles this chunk
     const int bh = blockIdx.x / a.nc, c = blockIdx.x % a.nc;
     const int b = bh / a.H, h = bh % a.H, t0 = c * C;
-    chunk_cumsum<J, GENERAL, NT>(a, b, h, t0, sG, sAux);
+    const Decay<J, GENERAL> dec{sDec};
+    load_decay<J, GENERAL, NT>(a, b, h, t0, dec);
     load_transposed<DT, D, VP, VLO, NT>((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, 0, t0, a.T, sVt[0],
                                     sVt[VLO ? 1 : 0], [](int, int) { return 1.f; });
     __syncthreads();
@@ -75,9 +89,6 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int qi = 32 * w + (lane & 31);  // chunk-relative query row of this lane
     const int tq = t0 + qi;
-    float range = 0.f;
-    for (int idx = lane; idx < C * J; idx += 64) range = fmaxf(range, fabsf(sG[idx]));
-    const bool safe = wave_max(range) <= kSafeRange;
 
     const in_t *qp = (const in_t *)a.q + b * a.q_sb + h * a.q_sh;
     const in_t *kp = (const in_t *)a.k + b * a.k_sb + h * a.k_sh;
@@ -107,7 +118,7 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
         float x[8];
         row8(qp, a.q_st, tq, ks, x);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(sG[qi * J + 16 * ks + 8 * hi + e] * kLog2e);
+        for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(dec.G(qi, 16 * ks + 8 * hi + e) * kLog2e);
         split8<OPB>(x, qh[ks], ql[ks]);
     }
 
@@ -121,14 +132,14 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
         f32x16 at;
 #pragma unroll
         for (int v = 0; v < 16; ++v) at[v] = 0.f;
-        if (safe) {
+        if constexpr (!FB) {
             const int kj = 32 * kb + (lane & 31);
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 float x[8];
                 row8(kp, a.k_st, t0 + kj, ks, x);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(-sG[kj * J + 16 * ks + 8 * hi + e] * kLog2e);
+                for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(-dec.G(kj, 16 * ks + 8 * hi + e) * kLog2e);
                 u32x4 kh, kl;
                 split8<OPB>(x, kh, kl);
                 at = mfma32<OPB>(kh, qh[ks], at);
@@ -139,14 +150,14 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
             // element-wise: A[q, k] = sum_c q_c k_c exp(G_q,c - G_k,c), every exponent <= 0
             for (int ch = 0; ch < J; ++ch) {
                 const float qv = tq < a.T ? to_f32<DT>(qp[(int64_t)tq * a.q_st + a.R + ch]) : 0.f;
-                const float gq = sG[qi * J + ch];
+                const float gq = dec.G(qi, ch);
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int kj = 32 * kb + 8 * (v / 4) + 4 * hi + (v % 4);
                     const int tk = t0 + kj;
                     if (kj <= qi && tk < a.T) {
                         const float kv = to_f32<DT>(kp[(int64_t)tk * a.k_st + a.R + ch]);
-                        at[v] = fmaf(qv * kv, fast_exp2((gq - sG[kj * J + ch]) * kLog2e), at[v]);
+                        at[v] = fmaf(qv * kv, fast_exp2((gq - dec.G(kj, ch)) * kLog2e), at[v]);
                     }
                 }
             }
@@ -236,7 +247,7 @@ bool rows_ok(const hofa_view_t &v, int es) {
 }
 
 struct WsLayout {
-    size_t ds, gl, sin, total;
+    size_t ds, gl, sin, flags, total;
 };
 
 WsLayout ws_layout(const hofa_gla_fwd_args_t *a) {
@@ -245,7 +256,8 @@ WsLayout ws_layout(const hofa_gla_fwd_args_t *a) {
     w.ds = 0;
     w.gl = (bh * nc * a->D * J * 4 + 255) / 256 * 256;
     w.sin = w.gl + (bh * nc * J * 4 + 255) / 256 * 256;
-    w.total = w.sin + (a->chunk_states ? 0 : (bh * nc * 2 * a->D * J * 2 + 255) / 256 * 256);
+    w.flags = w.sin + (a->chunk_states ? 0 : (bh * nc * 2 * a->D * J * 2 + 255) / 256 * 256);
+    w.total = w.flags + (bh * nc + 255) / 256 * 256;
     return w;
 }
 
@@ -282,7 +294,8 @@ void launch(const GlaK &k, hipStream_t s) {
     const int nblk = k.B * k.H * k.nc;
     hipLaunchKernelGGL((gla_state_kernel<DT, D, J, GEN, false>), dim3(nblk), dim3(kStateThreads), 0, s, k);
     hipLaunchKernelGGL((gla_scan_kernel<DT, D, J>), dim3(k.B * k.H, (D * J / 4 + 255) / 256), dim3(256), 0, s, k);
-    hipLaunchKernelGGL((gla_out_kernel<DT, D, J, GEN>), dim3(nblk), dim3(NT), 0, s, k);
+    hipLaunchKernelGGL((gla_out_kernel<DT, D, J, GEN, false>), dim3(nblk), dim3(NT), 0, s, k);
+    hipLaunchKernelGGL((gla_out_kernel<DT, D, J, GEN, true>), dim3(nblk), dim3(NT), 0, s, k);
 }
 
 template <int DT, bool GEN>
@@ -328,6 +341,7 @@ extern "C" int hofa_gla_fwd(const hofa_gla_fwd_args_t *a, void *workspace, size_
     k.ws_gl = (float *)(w + L.gl);
     k.s_in = a->chunk_states ? (uint16_t *)a->chunk_states : (uint16_t *)(w + L.sin);
     k.nplanes = a->chunk_states ? 4 : 2;
+    k.unsafe = (uint8_t *)(w + L.flags);
     k.n_out = (void *)a->n_out.data;
     k.rstd = a->n_out.data ? a->rstd : nullptr;
     k.n_sb = a->n_out.stride[0]; k.n_sh = a->n_out.stride[1]; k.n_st = a->n_out.stride[2];

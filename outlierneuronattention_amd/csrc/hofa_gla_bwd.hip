@@ -25,8 +25,11 @@
 //   3. gla_bwd_scan_kernel      reverse element-wise scan -> dH_end(c) as hi/lo planes
 //   4. gla_bwd_chunk_kernel     per chunk, 4 waves: 2 key-side waves (dk, dv),
 //                               2 query-side waves (dq); dGamma reductions
-//   5. gla_bwd_dlg_kernel       per head: later-chunk suffix of d log_gamma / d g
-//   6. gla_bwd_param_kernel     per head: d gla_scale, d log_alpha
+//                               (a factored launch and an element-wise launch for
+//                               chunks with a decay range beyond kSafeRange)
+//   5. gla_bwd_dlg_kernel       per (batch, head): later-chunk suffix of d log_gamma / d g,
+//                               d log_alpha and d gla_scale partials
+//   6. gla_bwd_param_kernel     per head: d gla_scale, d log_alpha (sum over the batch)
 // Every matrix-core product takes bf16 operands; computed operands are hi/lo
 // pairs (see split8) and raw f32/f16 inputs are split too, so products track fp32.
 #include "hofa_gla_common.h"
@@ -59,6 +62,8 @@ struct GlaBwdK {
     float *dlg_part;    // [B*H][T]
     float *chunk_part;  // [B*H][nc][2J+2]: sum_t dGamma, sum_t dGamma*Lin, e-total, log_gamma total
     float *dgs_part;    // [B*H][ntile][D]
+    float *part_la;     // [B*H][J]
+    float *part_gs;     // [B*H][D]
     int ntile;
 };
 
@@ -189,17 +194,30 @@ __global__ __launch_bounds__(256) void gla_bwd_scan_kernel(GlaBwdK a) {
     const int nc = a.f.nc;
     const int64_t base = (int64_t)bh * nc;
     f32x4 X = {0.f, 0.f, 0.f, 0.f};
-    for (int c = nc - 1; c >= 0; --c) {
-        store_state_planes<DT, D, J>(a.ds_end + (base + c) * 4 * D * J, 4, dv, j4, X);
-        const f32x4 dh = *(const f32x4 *)(a.ws_dh + (base + c) * D * J + dv * J + j4);
-        const f32x4 gl = *(const f32x4 *)(a.ws_gl + (base + c) * J + j4);
+    constexpr int PF = 4;  // chunks whose loads are in flight together
+    for (int c0 = nc - 1; c0 >= 0; c0 -= PF) {
+        f32x4 dh[PF], gl[PF];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) X[e] = fmaf(fast_exp2(gl[e] * kLog2e), X[e], dh[e]);
+        for (int u = 0; u < PF; ++u) {
+            const int c = max(c0 - u, 0);
+            dh[u] = *(const f32x4 *)(a.ws_dh + (base + c) * D * J + dv * J + j4);
+            gl[u] = *(const f32x4 *)(a.ws_gl + (base + c) * J + j4);
+        }
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            if (c0 - u < 0) break;
+            store_state_planes<DT, D, J>(a.ds_end + (base + c0 - u) * 4 * D * J, 4, dv, j4, X);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) X[e] = fmaf(fast_exp2(gl[u][e] * kLog2e), X[e], dh[u][e]);
+        }
     }
 }
 
 // ---------------------------------------------------------------- 4. chunk kernel
-template <int DT, int D, int J, bool GENERAL>
+// FB = false: chunks whose decay range is within kSafeRange (factored
+// operands); FB = true: the others (element-wise intra-chunk terms).  Both
+// are launched over every chunk and leave at once for the chunks of the other.
+template <int DT, int D, int J, bool GENERAL, bool FB>
 __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
     using in_t = typename Stor<DT>::type;
     constexpr int TP = C + 4;             // token pitch of the transposed tiles
@@ -210,24 +228,26 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
     constexpr int MB = D / 32;
     constexpr bool SPL = kRawSplit<DT>;   // raw f32/f16 inputs are split as well
     constexpr int NO = SPL ? 2 : 1;
-    __shared__ float sG[C * J];
-    __shared__ float sAux[C + J];
+    constexpr int DGP = J + 1;             // pitch of the dGamma tile
+    __shared__ float sDec[Decay<J, GENERAL>::kFloats];
     __shared__ __attribute__((aligned(16))) uint16_t sQK[2][2][JP * TP];  // [Q~^T | K~^T][hi | lo]
     __shared__ __attribute__((aligned(16))) uint16_t sOt[NO][D * TP];     // dO^T
-    static_assert(sizeof(sQK) >= sizeof(float) * C * J, "dGamma reuses the operand tiles");
+    static_assert(sizeof(sQK) >= sizeof(float) * C * DGP, "dGamma reuses the operand tiles");
 
     const int nc = a.f.nc, H = a.f.H, T = a.f.T, R = a.f.R;
     const int bh = blockIdx.x / nc, c = blockIdx.x % nc;
     const int b = bh / H, h = bh % H, t0 = c * C;
-    chunk_cumsum<J, GENERAL, NTB>(a.f, b, h, t0, sG, sAux);
+    if ((a.f.unsafe[blockIdx.x] != 0) != FB) return;  // the other launch handles this chunk
+    const Decay<J, GENERAL> dec{sDec};
+    load_decay<J, GENERAL, NTB>(a.f, b, h, t0, dec);
     const in_t *qp = (const in_t *)a.f.q + b * a.f.q_sb + h * a.f.q_sh;
     const in_t *kp = (const in_t *)a.f.k + b * a.f.k_sb + h * a.f.k_sh;
     const in_t *vp = (const in_t *)a.f.v + b * a.f.v_sb + h * a.f.v_sh;
     const in_t *dop = (const in_t *)a.ws_do + (int64_t)bh * T * D;
     load_transposed<DT, J, TP, true, NTB>(qp, a.f.q_st, R, t0, T, sQK[0][0], sQK[0][1],
-                                          [&](int t, int ch) { return fast_exp2(sG[t * J + ch] * kLog2e); });
+                                          [&](int t, int ch) { return fast_exp2(dec.G(t, ch) * kLog2e); });
     load_transposed<DT, J, TP, true, NTB>(kp, a.f.k_st, R, t0, T, sQK[1][0], sQK[1][1],
-                                          [&](int t, int ch) { return fast_exp2(-sG[t * J + ch] * kLog2e); });
+                                          [&](int t, int ch) { return fast_exp2(-dec.G(t, ch) * kLog2e); });
     load_transposed<DT, D, TP, SPL, NTB>(dop, D, 0, t0, T, sOt[0], sOt[NO - 1], [](int, int) { return 1.f; });
     if constexpr (JP > J) {
         for (int i = threadIdx.x; i < (JP - J) * TP; i += NTB) {
@@ -241,10 +261,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
 
     const int lane = threadIdx.x & 63, hi = lane >> 5, l32 = lane & 31;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float range = 0.f;
-    for (int idx = lane; idx < C * J; idx += 64) range = fmaxf(range, fabsf(sG[idx]));
-    const bool safe = wave_max(range) <= kSafeRange;
-    const float *gl = sG + (C - 1) * J;
+    constexpr bool safe = !FB;
     const uint16_t *sin = a.s_in + ((int64_t)bh * nc + c) * 4 * D * J;
     const uint16_t *dse = a.ds_end + ((int64_t)bh * nc + c) * 4 * D * J;
     auto qval = [&](int ti, int ch) { return t0 + ti < T ? to_f32<DT>(qp[(int64_t)(t0 + ti) * a.f.q_st + R + ch]) : 0.f; };
@@ -274,13 +291,13 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
             if (ts < T) raw_op8<DT>(vp + (int64_t)ts * a.f.v_st + 16 * ks + 8 * hi, vh[ks], vl[ks]);
         }
         u32x4 kth[KS], ktl[KS];  // K~ = k e^-G of this key
-        if (safe) {
+        if constexpr (safe) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 float x[8];
                 row8f<DT>(kp, a.f.k_st, ts, T, R + 16 * ks + 8 * hi, x);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(-sG[s * J + 16 * ks + 8 * hi + e] * kLog2e);
+                for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(-dec.G(s, 16 * ks + 8 * hi + e) * kLog2e);
                 split8<OPB>(x, kth[ks], ktl[ks]);
             }
         }
@@ -304,13 +321,13 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
                 }
             }
             // A[t, s] = sum_c q_tc k_sc e^(G_tc - G_sc)
-            if (safe) {
+            if constexpr (safe) {
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
                     float x[8];
                     row8f<DT>(qp, a.f.q_st, t0 + tr, T, R + 16 * ks + 8 * hi, x);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(sG[tr * J + 16 * ks + 8 * hi + e] * kLog2e);
+                    for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(dec.G(tr, 16 * ks + 8 * hi + e) * kLog2e);
                     u32x4 qh, ql;
                     split8<OPB>(x, qh, ql);
                     at = mfma32<OPB>(qh, kth[ks], at);
@@ -319,11 +336,11 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
                 }
             } else {
                 for (int ch = 0; ch < J; ++ch) {
-                    const float kv = kval(s, ch), gs_ = sG[s * J + ch];
+                    const float kv = kval(s, ch), gs_ = dec.G(s, ch);
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
                         const int ti = 32 * tb + crow(v, hi);
-                        if (ti >= s) at[v] = fmaf(qval(ti, ch) * kv, fast_exp2((sG[ti * J + ch] - gs_) * kLog2e), at[v]);
+                        if (ti >= s) at[v] = fmaf(qval(ti, ch) * kv, fast_exp2((dec.G(ti, ch) - gs_) * kLog2e), at[v]);
                     }
                 }
             }
@@ -347,7 +364,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
                     dvt[mb] = mfma32<OPB>(oa, al, dvt[mb]);
                     if constexpr (SPL) dvt[mb] = mfma32<OPB>(perm_a(&sOt[NO - 1][ro], ks4, hi), ah, dvt[mb]);
                 }
-                if (safe) {
+                if constexpr (safe) {
                     u32x4 mh, ml;
                     split8v<OPB>(mt, 8 * k2, mh, ml);
 #pragma unroll
@@ -360,7 +377,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
                     }
                 }
             }
-            if (!safe) {  // dk_sc += sum_t M[t, s] q_tc e^(G_tc - G_sc) over the tile's rows (both lane halves)
+            if constexpr (!safe) {  // dk_sc += sum_t M[t, s] q_tc e^(G_tc - G_sc) over the tile's rows (both lane halves)
                 f32x16 mo;
 #pragma unroll
                 for (int v = 0; v < 16; ++v) mo[v] = __shfl_xor(mt[v], 32);
@@ -370,24 +387,24 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
                     for (int vv = 0; vv < 16; ++vv) {
                         const int ch = 32 * jb + crow(vv, hi);
                         if (ch >= J) continue;
-                        const float gsc = sG[s * J + ch];
+                        const float gsc = dec.G(s, ch);
                         float x = 0.f;
                         for (int v = 0; v < 16; ++v) {
                             const int ta = 32 * tb + crow(v, hi), tbb = 32 * tb + crow(v, 1 - hi);
-                            if (ta >= s) x = fmaf(mt[v] * qval(ta, ch), fast_exp2((sG[ta * J + ch] - gsc) * kLog2e), x);
-                            if (tbb >= s) x = fmaf(mo[v] * qval(tbb, ch), fast_exp2((sG[tbb * J + ch] - gsc) * kLog2e), x);
+                            if (ta >= s) x = fmaf(mt[v] * qval(ta, ch), fast_exp2((dec.G(ta, ch) - gsc) * kLog2e), x);
+                            if (tbb >= s) x = fmaf(mo[v] * qval(tbb, ch), fast_exp2((dec.G(tbb, ch) - gsc) * kLog2e), x);
                         }
                         acc[jb][vv] += x;
                     }
             }
         }
-        if (safe) {
+        if constexpr (safe) {
 #pragma unroll
             for (int jb = 0; jb < JB; ++jb)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int ch = 32 * jb + crow(v, hi);
-                    acc[jb][v] = ch < J ? acc[jb][v] * fast_exp2(-sG[s * J + ch] * kLog2e) : 0.f;
+                    acc[jb][v] = ch < J ? acc[jb][v] * fast_exp2(-dec.G(s, ch) * kLog2e) : 0.f;
                 }
         }
         if (c < nc - 1) {  // state gradient from later chunks
@@ -410,7 +427,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int ch = 32 * jb + crow(v, hi);
-                    if (ch < J) acc[jb][v] = fmaf(fast_exp2((gl[ch] - sG[s * J + ch]) * kLog2e), x[v], acc[jb][v]);
+                    if (ch < J) acc[jb][v] = fmaf(fast_exp2((dec.last(ch) - dec.G(s, ch)) * kLog2e), x[v], acc[jb][v]);
                 }
             }
             // dv^T[d, s] += sum_c dH_end^T[d, c] K^[s, c]
@@ -421,7 +438,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int ch = 16 * ks + 8 * hi + e;
-                    x[e] *= fast_exp2((gl[ch] - sG[s * J + ch]) * kLog2e);
+                    x[e] *= fast_exp2((dec.last(ch) - dec.G(s, ch)) * kLog2e);
                 }
                 u32x4 kh, kl;
                 split8<OPB>(x, kh, kl);
@@ -479,7 +496,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
             for (int v = 0; v < 16; ++v)
                 if (32 * sb + crow(v, hi) > t) mt[v] = 0.f;
-            if (safe) {
+            if constexpr (safe) {
 #pragma unroll
                 for (int k2 = 0; k2 < 2; ++k2) {
                     const int ks4 = 2 * sb + k2;
@@ -504,12 +521,12 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
                     for (int vv = 0; vv < 16; ++vv) {
                         const int ch = 32 * jb + crow(vv, hi);
                         if (ch >= J) continue;
-                        const float gtc = sG[t * J + ch];
+                        const float gtc = dec.G(t, ch);
                         float x = 0.f;
                         for (int v = 0; v < 16; ++v) {
                             const int sa = 32 * sb + crow(v, hi), sbb = 32 * sb + crow(v, 1 - hi);
-                            if (sa <= t) x = fmaf(mt[v] * kval(sa, ch), fast_exp2((gtc - sG[sa * J + ch]) * kLog2e), x);
-                            if (sbb <= t) x = fmaf(mo[v] * kval(sbb, ch), fast_exp2((gtc - sG[sbb * J + ch]) * kLog2e), x);
+                            if (sa <= t) x = fmaf(mt[v] * kval(sa, ch), fast_exp2((gtc - dec.G(sa, ch)) * kLog2e), x);
+                            if (sbb <= t) x = fmaf(mo[v] * kval(sbb, ch), fast_exp2((gtc - dec.G(sbb, ch)) * kLog2e), x);
                         }
                         acc[jb][vv] += x;
                     }
@@ -536,7 +553,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int ch = 32 * jb + crow(v, hi);
-                const float eg = ch < J ? fast_exp2(sG[t * J + ch] * kLog2e) : 0.f;
+                const float eg = ch < J ? fast_exp2(dec.G(t, ch) * kLog2e) : 0.f;
                 acc[jb][v] = safe ? eg * (acc[jb][v] + x[v]) : fmaf(eg, x[v], acc[jb][v]);
             }
         }
@@ -561,7 +578,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int ch = 32 * jb + crow(v, hi);
-                if (ch < J) sDG[tok * J + ch] = qval(tok, ch) * acc[jb][v];
+                if (ch < J) sDG[tok * DGP + ch] = qval(tok, ch) * acc[jb][v];
             }
     }
     __syncthreads();
@@ -571,16 +588,16 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int ch = 32 * jb + crow(v, hi);
-                if (ch < J) sDG[tok * J + ch] -= kval(tok, ch) * acc[jb][v];
+                if (ch < J) sDG[tok * DGP + ch] -= kval(tok, ch) * acc[jb][v];
             }
     }
     __syncthreads();
     float *cp = a.chunk_part + ((int64_t)bh * nc + c) * (2 * J + 2);
     if constexpr (!GENERAL) {
-        const float *sLam = sAux, *sAl = sAux + C;
+        const float *sLam = sDec, *sAl = sDec + C;
         if (w == 0) {
             float e = 0.f;
-            for (int ch = 0; ch < J; ++ch) e = fmaf(sAl[ch], sDG[lane * J + ch], e);
+            for (int ch = 0; ch < J; ++ch) e = fmaf(sAl[ch], sDG[lane * DGP + ch], e);
 #pragma unroll
             for (int off = 1; off < 64; off <<= 1) {
                 const float y = __shfl_down(e, off);
@@ -595,7 +612,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
         for (int ch = threadIdx.x; ch < J; ch += NTB) {
             float ed = 0.f, f = 0.f;
             for (int t = 0; t < C; ++t) {
-                const float x = sDG[t * J + ch];
+                const float x = sDG[t * DGP + ch];
                 ed += x;
                 f = fmaf(x, sLam[t], f);
             }
@@ -607,7 +624,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
         for (int ch = threadIdx.x; ch < J; ch += NTB) {
             float s = 0.f;
             for (int t = C - 1; t >= 0; --t) {
-                s += sDG[t * J + ch];
+                s += sDG[t * DGP + ch];
                 if (t0 + t < T) dg[(int64_t)(t0 + t) * a.dg_st + ch * a.dg_sj] = s;
             }
             cp[ch] = s;
@@ -615,20 +632,26 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
     }
 }
 
-// ---------------------------------------------------------------- 5. later-chunk suffix
-template <int J, bool GENERAL>
+// ---------------------------------------------------------------- 5. per-head suffix and partials
+// One block per (b, h): adds the later-chunk suffix to d log_gamma (or d g),
+// and reduces this head's d log_alpha / d gla_scale partials over chunks and
+// token tiles.
+template <int D, int J, bool GENERAL>
 __global__ __launch_bounds__(256) void gla_bwd_dlg_kernel(GlaBwdK a) {
-    __shared__ float sSfx[kMaxChunks];
+    __shared__ float sSfx[kMaxChunks];   // sum of e over later chunks
+    __shared__ float sLst[kMaxChunks];   // cumsum of log_gamma before the chunk
+    __shared__ float sRed[256];
+    constexpr int CPS = 2 * J + 2;
     const int bh = blockIdx.x, H = a.f.H, T = a.f.T, nc = a.f.nc;
     const int b = bh / H, h = bh % H;
-    const int tid = threadIdx.x, lane = tid & 63;
-    float *cp = a.chunk_part + (int64_t)bh * nc * (2 * J + 2);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    float *cp = a.chunk_part + (int64_t)bh * nc * CPS;
     if constexpr (!GENERAL) {
-        if (tid < 64) {
+        if (w == 0) {  // exclusive suffix of the per-chunk e totals
             float carry = 0.f;
             for (int top = nc - 1; top >= 0; top -= 64) {
                 const int c = top - lane;
-                const float e = c >= 0 ? cp[(int64_t)c * (2 * J + 2) + 2 * J] : 0.f;
+                const float e = c >= 0 ? cp[(int64_t)c * CPS + 2 * J] : 0.f;
                 float x = e;
 #pragma unroll
                 for (int off = 1; off < 64; off <<= 1) {
@@ -638,16 +661,47 @@ __global__ __launch_bounds__(256) void gla_bwd_dlg_kernel(GlaBwdK a) {
                 if (c >= 0) sSfx[c] = carry + x - e;
                 carry += __shfl(x, 63);
             }
+        } else if (w == 1) {  // exclusive prefix of the per-chunk log_gamma totals
+            float carry = 0.f;
+            for (int c0 = 0; c0 < nc; c0 += 64) {
+                const int c = c0 + lane;
+                const float l = c < nc ? cp[(int64_t)c * CPS + 2 * J + 1] : 0.f;
+                float x = l;
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1) {
+                    const float y = __shfl_up(x, off);
+                    if (lane >= off) x += y;
+                }
+                if (c < nc) sLst[c] = carry + x - l;
+                carry += __shfl(x, 63);
+            }
         }
         __syncthreads();
         for (int t = tid; t < T; t += 256)
             store_any(a.dlg, a.dlg_dt, b * a.dlg_sb + h * a.dlg_sh + (int64_t)t * a.dlg_st,
                       a.dlg_part[(int64_t)bh * T + t] + sSfx[t / C]);
+        if (a.dla) {  // sum_c (Lambda_start(c) sum_t dGamma + sum_t dGamma Lambda_in), channel-parallel
+            constexpr int NSEG = 256 / J;
+            const int ch = tid % J, seg = tid / J;
+            float acc = 0.f;
+            if (seg < NSEG)
+                for (int c = seg; c < nc; c += NSEG) {
+                    const float *p = cp + (int64_t)c * CPS;
+                    acc = fmaf(sLst[c], p[ch], acc + p[J + ch]);
+                }
+            sRed[tid] = acc;
+            __syncthreads();
+            if (tid < J) {
+                float t = 0.f;
+                for (int sg = 0; sg < NSEG; ++sg) t += sRed[sg * J + tid];
+                a.part_la[(int64_t)bh * J + tid] = t;
+            }
+        }
     } else {
         for (int ch = tid; ch < J; ch += 256) {
             float carry = 0.f;
             for (int c = nc - 1; c >= 0; --c) {
-                float *p = cp + (int64_t)c * (2 * J + 2) + ch;
+                float *p = cp + (int64_t)c * CPS + ch;
                 const float x = *p;
                 *p = carry;
                 carry += x;
@@ -657,35 +711,31 @@ __global__ __launch_bounds__(256) void gla_bwd_dlg_kernel(GlaBwdK a) {
         float *dg = (float *)a.dg + b * a.dg_sb + h * a.dg_sh;
         for (int64_t i = tid; i < (int64_t)T * J; i += 256) {
             const int t = (int)(i / J), ch = (int)(i % J);
-            dg[(int64_t)t * a.dg_st + ch * a.dg_sj] += cp[(int64_t)(t / C) * (2 * J + 2) + ch];
+            dg[(int64_t)t * a.dg_st + ch * a.dg_sj] += cp[(int64_t)(t / C) * CPS + ch];
         }
+    }
+    for (int d = tid; d < D; d += 256) {
+        float s = 0.f;
+        for (int tile = 0; tile < a.ntile; ++tile) s += a.dgs_part[((int64_t)bh * a.ntile + tile) * D + d];
+        a.part_gs[(int64_t)bh * D + d] = s;
     }
 }
 
 // ---------------------------------------------------------------- 6. per-head parameters
 template <int D, int J, bool GENERAL>
 __global__ __launch_bounds__(256) void gla_bwd_param_kernel(GlaBwdK a) {
-    const int h = blockIdx.x, H = a.f.H, B = a.f.B, nc = a.f.nc;
+    const int h = blockIdx.x, H = a.f.H, B = a.f.B;
     for (int d = threadIdx.x; d < D; d += 256) {
         float s = 0.f;
-        for (int b = 0; b < B; ++b)
-            for (int tile = 0; tile < a.ntile; ++tile) s += a.dgs_part[((int64_t)(b * H + h) * a.ntile + tile) * D + d];
+        for (int b = 0; b < B; ++b) s += a.part_gs[(int64_t)(b * H + h) * D + d];
         store_any(a.dgs, a.dgs_dt, h * a.dgs_sh + d * a.dgs_sd, s);
     }
     if constexpr (!GENERAL) {
         if (!a.dla) return;
         for (int ch = threadIdx.x; ch < J; ch += 256) {
-            const float alpha = expf(load_any(a.f.la, a.f.la_dt, h * a.f.la_sh + ch * a.f.la_sj));
             float s = 0.f;
-            for (int b = 0; b < B; ++b) {
-                const float *cp = a.chunk_part + (int64_t)(b * H + h) * nc * (2 * J + 2);
-                float lam = 0.f;  // cumsum of log_gamma before the chunk
-                for (int c = 0; c < nc; ++c) {
-                    const float *p = cp + (int64_t)c * (2 * J + 2);
-                    s += fmaf(lam, p[ch], p[J + ch]);
-                    lam += p[2 * J + 1];
-                }
-            }
+            for (int b = 0; b < B; ++b) s += a.part_la[(int64_t)(b * H + h) * J + ch];
+            const float alpha = expf(load_any(a.f.la, a.f.la_dt, h * a.f.la_sh + ch * a.f.la_sj));
             store_any(a.dla, a.dla_dt, h * a.dla_sh + ch * a.dla_sj, alpha * s);
         }
     }
@@ -702,7 +752,7 @@ bool rows_ok(const hofa_view_t &v, int es) {
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 struct WsLayout {
-    size_t dO, dh, gl, dse, dlg, cp, dgs, total;
+    size_t dO, dh, gl, dse, dlg, cp, dgs, pla, pgs, flags, total;
 };
 
 WsLayout ws_layout(const hofa_gla_bwd_args_t *a) {
@@ -716,7 +766,10 @@ WsLayout ws_layout(const hofa_gla_bwd_args_t *a) {
     w.dlg = w.dse + align256(bh * nc * 4 * D * J * 2);
     w.cp = w.dlg + align256(bh * T * 4);
     w.dgs = w.cp + align256(bh * nc * (2 * J + 2) * 4);
-    w.total = w.dgs + align256(bh * ntile * D * 4);
+    w.pla = w.dgs + align256(bh * ntile * D * 4);
+    w.pgs = w.pla + align256(bh * J * 4);
+    w.flags = w.pgs + align256(bh * D * 4);
+    w.total = w.flags + align256(bh * nc);
     return w;
 }
 
@@ -774,8 +827,9 @@ void launch(const GlaBwdK &k, hipStream_t s) {
     fk.ws_gl = k.ws_gl;
     hipLaunchKernelGGL((gla_state_kernel<DT, D, J, GEN, true>), dim3(nbh * k.f.nc), dim3(kStateThreads), 0, s, fk);
     hipLaunchKernelGGL((gla_bwd_scan_kernel<DT, D, J>), dim3(nbh, (D * J / 4 + 255) / 256), dim3(256), 0, s, k);
-    hipLaunchKernelGGL((gla_bwd_chunk_kernel<DT, D, J, GEN>), dim3(nbh * k.f.nc), dim3(NTB), 0, s, k);
-    hipLaunchKernelGGL((gla_bwd_dlg_kernel<J, GEN>), dim3(nbh), dim3(256), 0, s, k);
+    hipLaunchKernelGGL((gla_bwd_chunk_kernel<DT, D, J, GEN, false>), dim3(nbh * k.f.nc), dim3(NTB), 0, s, k);
+    hipLaunchKernelGGL((gla_bwd_chunk_kernel<DT, D, J, GEN, true>), dim3(nbh * k.f.nc), dim3(NTB), 0, s, k);
+    hipLaunchKernelGGL((gla_bwd_dlg_kernel<D, J, GEN>), dim3(nbh), dim3(256), 0, s, k);
     hipLaunchKernelGGL((gla_bwd_param_kernel<D, J, GEN>), dim3(k.f.H), dim3(256), 0, s, k);
 }
 
@@ -854,6 +908,9 @@ extern "C" int hofa_gla_bwd(const hofa_gla_bwd_args_t *a, void *workspace, size_
     k.dlg_part = (float *)(w + L.dlg);
     k.chunk_part = (float *)(w + L.cp);
     k.dgs_part = (float *)(w + L.dgs);
+    k.part_la = (float *)(w + L.pla);
+    k.part_gs = (float *)(w + L.pgs);
+    f.unsafe = (uint8_t *)(w + L.flags);
     k.ntile = (a->T + ET - 1) / ET;
     const int J = a->D - a->R;
     hipStream_t s = (hipStream_t)stream;

@@ -52,6 +52,7 @@ struct GlaK {
     float *ws_ds;       // [B*H][nc][D][J] f32 per-chunk outer products
     float *ws_gl;       // [B*H][nc][J] f32 per-chunk total log decay
     uint16_t *s_in;     // [B*H][nc][nplanes][D*J] entering states as 16-bit hi/lo planes
+    uint8_t *unsafe;    // [B*H*nc] per chunk: decay range beyond kSafeRange (set by gla_state_kernel)
     int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, y_sb, y_sh, y_st;
     int64_t n_sb, n_sh, n_st;
     int64_t lg_sb, lg_sh, lg_st, la_sh, la_sj, g_sb, g_sh, g_st, g_sj;
@@ -65,40 +66,98 @@ struct GlaK {
     float eps;
 };
 
-// In-chunk inclusive cumsum of the log decay into sG[C][J] (tokens past T
-// decay by 0).  Scalar decay also leaves the cumsum of log_gamma in
-// sAux[0..C) and exp(log_alpha) in sAux[C..C+J).
+// In-chunk inclusive cumsum G[t][c] of the log decay (t < C, c < J), in LDS.
+// Scalar decay keeps two vectors and forms G = Lambda[t] * alpha[c] on the fly
+// (Lambda = in-chunk cumsum of log_gamma, alpha = exp(log_alpha)); general
+// decay keeps a [C][J+1] table, the odd pitch spreading lane-per-token reads
+// over all banks.  Tokens past T decay by 0.  Eight trailing floats hold the
+// per-wave partial maxima behind range().
+template <int J, bool GENERAL>
+struct Decay {
+    static constexpr int GP = J + 1;
+    static constexpr int kBody = GENERAL ? C * GP : C + J;
+    static constexpr int kFloats = kBody + 8;
+    float *s;
+    __device__ __forceinline__ float G(int t, int c) const {
+        if constexpr (GENERAL) return s[t * GP + c];
+        else return s[t] * s[C + c];
+    }
+    __device__ __forceinline__ float last(int c) const { return G(C - 1, c); }
+    // Largest |G| over the chunk (valid after load_decay).
+    __device__ __forceinline__ float range() const {
+        const float *r = s + kBody;
+        if constexpr (GENERAL) return fmaxf(fmaxf(r[0], r[1]), fmaxf(r[2], r[3]));
+        else return r[0] * r[1];
+    }
+};
+
+// Fill a Decay for chunk [t0, t0+C) of head (b, h); ends with a barrier.  NTH
+// threads, 128 <= NTH <= 256.
 template <int J, bool GENERAL, int NTH>
-__device__ void chunk_cumsum(const GlaK &a, int b, int h, int t0, float *sG, float *sAux) {
-    const int tid = threadIdx.x;
+__device__ void load_decay(const GlaK &a, int b, int h, int t0, Decay<J, GENERAL> dec) {
+    static_assert(NTH >= 128 && NTH <= 256, "two to four waves");
+    constexpr int NW = NTH / 64;
+    float *s = dec.s, *red = s + Decay<J, GENERAL>::kBody;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     if constexpr (!GENERAL) {
-        float *sLam = sAux, *sAl = sAux + C;
-        if (tid < 64) {
-            const int t = t0 + tid;
+        if (w == 0) {
+            const int t = t0 + lane;
             float x = t < a.T ? load_any(a.lg, a.lg_dt, b * a.lg_sb + h * a.lg_sh + (int64_t)t * a.lg_st) : 0.f;
 #pragma unroll
             for (int off = 1; off < 64; off <<= 1) {
                 const float y = __shfl_up(x, off);
-                if (tid >= off) x += y;
+                if (lane >= off) x += y;
             }
-            sLam[tid] = x;
+            s[lane] = x;
+            const float m = wave_max(fabsf(x));
+            if (lane == 0) red[0] = m;
+        } else if (w == 1) {
+            float m = 0.f;
+            for (int c = lane; c < J; c += 64) {
+                const float al = a.la ? expf(load_any(a.la, a.la_dt, h * a.la_sh + c * a.la_sj)) : 1.f;
+                s[C + c] = al;
+                m = fmaxf(m, al);
+            }
+            m = wave_max(m);
+            if (lane == 0) red[1] = m;
         }
-        for (int c = tid; c < J; c += NTH) sAl[c] = a.la ? expf(load_any(a.la, a.la_dt, h * a.la_sh + c * a.la_sj)) : 1.f;
         __syncthreads();
-        for (int idx = tid; idx < C * J; idx += NTH) sG[idx] = sLam[idx / J] * sAl[idx % J];
     } else {
         const float *gp = (const float *)a.g + b * a.g_sb + h * a.g_sh;
-        for (int c = tid; c < J; c += NTH) {
-            float acc = 0.f;
-#pragma unroll 8
-            for (int t = 0; t < C; ++t) {
-                const int tt = t0 + t;
-                acc += tt < a.T ? gp[(int64_t)tt * a.g_st + c * a.g_sj] : 0.f;
-                sG[t * J + c] = acc;
+        const bool vec = a.g_sj == 1 && (a.g_st % 4) == 0 && (a.g_sb % 4) == 0 && (a.g_sh % 4) == 0 &&
+                         ((uintptr_t)a.g % 16) == 0;
+        for (int idx = tid; idx < C * J / 4; idx += NTH) {
+            const int t = idx / (J / 4), c = 4 * (idx % (J / 4));
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            if (t0 + t < a.T) {
+                const float *p = gp + (int64_t)(t0 + t) * a.g_st;
+                if (vec) {
+                    x = *(const f32x4 *)(p + c);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) x[e] = p[(c + e) * a.g_sj];
+                }
             }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[t * Decay<J, GENERAL>::GP + c + e] = x[e];
         }
+        if (tid < 4) red[tid] = 0.f;
+        __syncthreads();
+        float m = 0.f;
+        for (int c = w; c < J; c += NW) {  // one column per wave pass: lane = token
+            float x = s[lane * Decay<J, GENERAL>::GP + c];
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float y = __shfl_up(x, off);
+                if (lane >= off) x += y;
+            }
+            s[lane * Decay<J, GENERAL>::GP + c] = x;
+            m = fmaxf(m, fabsf(x));
+        }
+        m = wave_max(m);
+        if (lane == 0) red[w] = m;
+        __syncthreads();
     }
-    __syncthreads();
 }
 
 // Copy one chunk of rows [t0, t0+C) x columns [col0, col0+W) into LDS
@@ -153,28 +212,29 @@ constexpr int kStateThreads = 128;
 //   backward (BWD=true): out^T[D x J] = dO_c^T (Q_c (.) exp(G))
 // with the key operand read at columns [key_col0, key_col0+J) of a.k and the
 // value operand from a.v (every exponent <= 0).  Writes out^T to ws_ds and
-// G_last to ws_gl.  2 waves, v_mfma_f32_16x16x32 tiles, hi/lo split operands.
+// G_last to ws_gl, and whether the chunk's decay range exceeds kSafeRange to
+// unsafe[].  2 waves, v_mfma_f32_16x16x32 tiles, hi/lo split operands.
 template <int DT, int D, int J, bool GENERAL, bool BWD>
 __global__ __launch_bounds__(kStateThreads) void gla_state_kernel(GlaK a) {
     using in_t = typename Stor<DT>::type;
     constexpr int NTH = kStateThreads;
     constexpr int TP = C + 8;               // token pitch of the transposed tiles
     constexpr bool VLO = kRawSplit<DT>;     // f32/f16 inputs also split the value operand
-    __shared__ float sG[C * J];
-    __shared__ float sAux[C + J];
+    __shared__ float sDec[Decay<J, GENERAL>::kFloats];
     __shared__ __attribute__((aligned(16))) uint16_t sKt[2][J * TP];
     __shared__ __attribute__((aligned(16))) uint16_t sVt[VLO ? 2 : 1][D * TP];
     const int bh = blockIdx.x / a.nc, c = blockIdx.x % a.nc;
     const int b = bh / a.H, h = bh % a.H, t0 = c * C;
-    chunk_cumsum<J, GENERAL, NTH>(a, b, h, t0, sG, sAux);
-    const float *gl = sG + (C - 1) * J;
+    const Decay<J, GENERAL> dec{sDec};
+    load_decay<J, GENERAL, NTH>(a, b, h, t0, dec);
+    if (threadIdx.x == 0) a.unsafe[blockIdx.x] = dec.range() > kSafeRange;
     const in_t *kb = (const in_t *)a.k + b * a.k_sb + h * a.k_sh;
     if constexpr (BWD)
         load_transposed<DT, J, TP, true, NTH>(kb, a.k_st, a.key_col0, t0, a.T, sKt[0], sKt[1],
-                                              [&](int t, int ch) { return fast_exp2(sG[t * J + ch] * kLog2e); });
+                                              [&](int t, int ch) { return fast_exp2(dec.G(t, ch) * kLog2e); });
     else
         load_transposed<DT, J, TP, true, NTH>(kb, a.k_st, a.key_col0, t0, a.T, sKt[0], sKt[1], [&](int t, int ch) {
-            return fast_exp2((gl[ch] - sG[t * J + ch]) * kLog2e);
+            return fast_exp2((dec.last(ch) - dec.G(t, ch)) * kLog2e);
         });
     load_transposed<DT, D, TP, VLO, NTH>((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, 0, t0, a.T, sVt[0],
                                          sVt[VLO ? 1 : 0], [](int, int) { return 1.f; });
@@ -198,7 +258,7 @@ __global__ __launch_bounds__(kStateThreads) void gla_state_kernel(GlaK a) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) ds[(16 * tm + 4 * g4 + v) * J + 16 * tn + r16] = acc[v];
     }
-    for (int ch = threadIdx.x; ch < J; ch += NTH) a.ws_gl[((int64_t)bh * a.nc + c) * J + ch] = gl[ch];
+    for (int ch = threadIdx.x; ch < J; ch += NTH) a.ws_gl[((int64_t)bh * a.nc + c) * J + ch] = dec.last(ch);
 }
 
 // hi/lo 16-bit planes of 4 consecutive floats.

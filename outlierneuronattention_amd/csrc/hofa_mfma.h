@@ -41,15 +41,19 @@ __device__ __forceinline__ f32x4 mfma16(const u32x4 &a, const u32x4 &b, const f3
     }
 }
 
-// Two floats -> one dword of 16-bit operands (lo in bits 0..15).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> one dword of 16-bit operands (lo in bits 0..15), round to
+// nearest even; one packed conversion instruction.
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    const f32x2 v = {lo, hi};
     if constexpr (kF16Ops<DT>) {
-        return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
     } else {
-        return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
     }
 }
 

@@ -183,3 +183,29 @@ def test_attention_backward_alone_matches_torch():
     torch.cuda.synchronize()
     for out, ref, name in ((dq, leaves[0].grad, "dq"), (dk, leaves[1].grad, "dk"), (dv, leaves[2].grad, "dv")):
         _check(out, ref, 2e-2, name)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_hofa_core_backward_shared_outlier_channels(dtype):
+    """``q_o = k_o = None``: the outlier channels are q[..., :r], k[..., :r]
+    (no RoPE); the attention gradient is written into dq/dk[..., :r] in place."""
+    from outlierneuronattention_amd.autograd import hofa_core
+    B, H, T, D, R = 2, 2, 180, 64, 16
+    x, dy = _inputs(B, H, T, D, R, True, True, 1.0, dtype, seed=99)
+    sm = math.sqrt(D / R)
+    leaves = {k: (t.double().requires_grad_() if t is not None else None) for k, t in x.items()}
+    q, k, v = leaves["q"], leaves["k"], leaves["v"]
+    g = decay_from_gates(leaves["log_gamma"], D - R, leaves["log_alpha"])
+    yi, _ = gla_chunked(q[..., R:], k[..., R:], v, g)
+    m = leaves["mix"].unsqueeze(-1)
+    y = (1 - m) * rmsnorm(yi, FP32_EPS) * leaves["gla_scale"] + m * outlier_attention(q[..., :R], k[..., :R], v, sm)
+    y.backward(dy.double())
+    dev = {kk: (t.to(DEV, torch.float32 if kk in ("log_alpha", "gla_scale") else dtype).requires_grad_()
+                if t is not None else None) for kk, t in x.items()}
+    out = hofa_core(None, None, dev["q"], dev["k"], dev["v"], dev["log_gamma"], dev["log_alpha"], dev["mix"],
+                    dev["gla_scale"], R, sm)
+    out.backward(dy.to(DEV, dtype))
+    torch.cuda.synchronize()
+    tol = 2e-2
+    for name in ("q", "k", "v", "log_gamma", "log_alpha", "mix", "gla_scale"):
+        _check(dev[name].grad, leaves[name].grad, tol, f"d{name}")

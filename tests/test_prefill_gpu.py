@@ -6,8 +6,11 @@ Tolerances:
   <= 2e-2 (outputs are O(1)); f32 inputs (bf16 matrix operands): 3e-2.
 * GLA final state (fp32 accumulation of bf16 products): relative L2 <= 1e-3
   against the float64 oracle on the same rounded inputs.
-* base-2 log-sum-exp of the attention rows: max-abs <= 1e-3 (fp32 softmax
-  statistics).
+* base-2 log-sum-exp of the attention rows: f32 inputs max-abs <= 1e-3 (f32
+  row sums); bf16/f16 inputs max-abs <= 6e-3: their row sum is taken on the
+  matrix core over the same 16-bit rounded probabilities that form O (so O is
+  normalised consistently), and each rounded probability carries a relative
+  error of at most 2^-8, i.e. log2(1 + 2^-8) = 5.6e-3 on the sum.
 """
 import math
 
@@ -67,7 +70,8 @@ def test_exact_attention_matches_oracle(B, H, T, D, R, dtype):
     assert (_c(o) - O).abs().max().item() <= tol
     expect = _c(prior) + _c(mix) * O
     assert (_c(out) - expect).abs().max().item() <= tol
-    assert (lse.cpu().double().view(B, H, T) - L * LOG2E).abs().max().item() <= 1e-3
+    lse_tol = 1e-3 if dtype == torch.float32 else 6e-3
+    assert (lse.cpu().double().view(B, H, T) - L * LOG2E).abs().max().item() <= lse_tol
     # without `out`: a fresh mix*O
     fresh = exact_attention(q, k, v, R, sm, mix)
     torch.cuda.synchronize()
