@@ -87,25 +87,25 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnFwdK a) {
     // slots so a tile's loads have two tile-iterations to arrive
     u32x4 kreg[2][NKC], klo[2][NKC];
     u32x4 vreg[2][NVP][2];
+    constexpr int ES = sizeof(in_t);
+    const __amdgpu_buffer_rsrc_t rk = rows_rsrc(kp, (uint32_t)(a.T * a.k_st * ES));
+    const __amdgpu_buffer_rsrc_t rv = rows_rsrc(vp, (uint32_t)(a.T * a.v_st * ES));
     auto gload = [&](int kt, int sl) {
         const int k0 = kt * BN;
 #pragma unroll
         for (int i = 0; i < NKC; ++i) {
-            const int ci = tid + NT * i;
+            const int ci = min(tid + NT * i, KCH - 1);  // threads past the tile reload its last chunk
             const int row = ci / (R / 8), part = ci % (R / 8);
-            const int key = k0 + row;
-            kreg[sl][i] = (ci < KCH && key < a.T) ? load_op8<DT>(kp + (int64_t)key * a.k_st + 8 * part) : u32x4{0, 0, 0, 0};
-            if constexpr (SPLIT)
-                klo[sl][i] = (ci < KCH && key < a.T) ? load_lo8_f32((const float *)kp + (int64_t)key * a.k_st + 8 * part)
-                                                     : u32x4{0, 0, 0, 0};
+            const uint32_t off = (uint32_t)(((k0 + row) * a.k_st + 8 * part) * ES);
+            kreg[sl][i] = bload_op8<DT>(rk, off, SPLIT ? &klo[sl][i] : nullptr);
         }
 #pragma unroll
         for (int i = 0; i < NVP; ++i) {
             const int pi = tid + NT * i;
             const int kpair = pi / (D / 8), cch = pi % (D / 8);
-            const int key = k0 + 2 * kpair;
-            vreg[sl][i][0] = key < a.T ? load_op8<DT>(vp + (int64_t)key * a.v_st + 8 * cch) : u32x4{0, 0, 0, 0};
-            vreg[sl][i][1] = key + 1 < a.T ? load_op8<DT>(vp + (int64_t)(key + 1) * a.v_st + 8 * cch) : u32x4{0, 0, 0, 0};
+            const uint32_t off = (uint32_t)(((k0 + 2 * kpair) * a.v_st + 8 * cch) * ES);
+            vreg[sl][i][0] = bload_op8<DT>(rv, off);
+            vreg[sl][i][1] = bload_op8<DT>(rv, off + (uint32_t)(a.v_st * ES));
         }
     };
     auto lstore = [&](int buf, int sl) {
@@ -151,8 +151,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnFwdK a) {
         f32x16 s[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) s[kb][v] = 0.f;
+            s[kb] = f32x16{};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 const u32x4 ka = *(const u32x4 *)&sK[buf][(32 * kb + (lane & 31)) * KP + 16 * ks + 8 * hi];
@@ -165,13 +164,12 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnFwdK a) {
             }
         }
         if (k0 + BN - 1 > qw0 || k0 + BN > a.T) {  // tile crosses the diagonal or the end
+            const int lim = min(qrow, a.T - 1) - k0 - 4 * hi;  // visible iff row offset <= lim
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int key = k0 + 32 * kb + 8 * (v / 4) + 4 * hi + (v % 4);
-                    if (key > qrow || key >= a.T) s[kb][v] = -INFINITY;
-                }
+                for (int v = 0; v < 16; ++v)
+                    s[kb][v] = 32 * kb + 8 * (v / 4) + (v % 4) <= lim ? s[kb][v] : -INFINITY;
         }
         float t8[8];  // max as a tree (short dependency chains)
 #pragma unroll
@@ -307,6 +305,9 @@ extern "C" int hofa_attn_fwd(const hofa_attn_fwd_args_t *a, void *stream) {
                  HOFA_EINVAL, "hofa_attn_fwd: q/k/v/y/o need unit last stride and 16-byte aligned rows");
     HOFA_REQUIRE(!a->mix.data || a->mix.dtype == HOFA_F32 || a->mix.dtype == HOFA_BF16 || a->mix.dtype == HOFA_F16,
                  HOFA_EINVAL, "hofa_attn_fwd: bad mix dtype");
+    HOFA_REQUIRE((int64_t)(a->T + 2 * BN) * a->k.stride[2] * es < (1ll << 31) &&
+                     (int64_t)(a->T + 2 * BN) * a->v.stride[2] * es < (1ll << 31),
+                 HOFA_EUNSUPPORTED, "hofa_attn_fwd: one head's K/V rows must span less than 2 GiB");
     AttnFwdK k{};
     k.q = a->q.data; k.k = a->k.data; k.v = a->v.data; k.mix = a->mix.data;
     k.y = (void *)a->y.data; k.o = (void *)a->o.data; k.lse = a->lse;

@@ -43,38 +43,62 @@ struct AttnBwdK {
     float sm_scale;
 };
 
-// Rows [t0, t0+64) of a [T, W] operand matrix into LDS row-major ([64][W + pad])
-// and/or transposed ([W][64 + pad]); rows past T are zero.  256 threads.
-// With LO (f32 input) the row-major bf16 rounding remainders go to lo.
-template <int DT, int W, int PR, int PT, bool ROW, bool TR, bool LO = false>
-__device__ void stage_rows(const typename Stor<DT>::type *base, int64_t st, int t0, int T, uint16_t *row,
-                           uint16_t *tr, uint16_t *lo = nullptr) {
-    constexpr int NPIECE = 32 * (W / 8);  // (2 rows x 8 columns) pieces
-    for (int pi = threadIdx.x; pi < NPIECE; pi += NT) {
-        const int rp = pi / (W / 8), cc = pi % (W / 8);
-        const int r0 = 2 * rp;
-        u32x4 x0 = {0, 0, 0, 0}, x1 = {0, 0, 0, 0};
-        if (t0 + r0 < T) x0 = load_op8<DT>(base + (int64_t)(t0 + r0) * st + 8 * cc);
-        if (t0 + r0 + 1 < T) x1 = load_op8<DT>(base + (int64_t)(t0 + r0 + 1) * st + 8 * cc);
-        if constexpr (ROW) {
-            *(u32x4 *)&row[r0 * PR + 8 * cc] = x0;
-            *(u32x4 *)&row[(r0 + 1) * PR + 8 * cc] = x1;
-        }
-        if constexpr (LO && DT == HOFA_F32) {
-            const u32x4 z = {0, 0, 0, 0};
-            *(u32x4 *)&lo[r0 * PR + 8 * cc] = t0 + r0 < T ? load_lo8_f32(base + (int64_t)(t0 + r0) * st + 8 * cc) : z;
-            *(u32x4 *)&lo[(r0 + 1) * PR + 8 * cc] =
-                t0 + r0 + 1 < T ? load_lo8_f32(base + (int64_t)(t0 + r0 + 1) * st + 8 * cc) : z;
-        }
-        if constexpr (TR) {
+// Rows [t0, t0+64) of a [T, W] operand matrix, staged global -> registers
+// (fetch, issued a tile ahead) -> LDS (put): row-major ([64][W + pad]) and/or
+// transposed ([W][64 + pad]) 16-bit operands, rows past T zero; f32 inputs
+// also keep their bf16 rounding remainders (row-major).  256 threads, each
+// owning (2 rows x 8 columns) pieces.
+template <int DT, int W>
+struct RowStage {
+    using in_t = typename Stor<DT>::type;
+    static constexpr int NPIECE = 32 * (W / 8);
+    static constexpr int NP = (NPIECE + NT - 1) / NT;
+    static constexpr bool LO = DT == HOFA_F32;
+    u32x4 x0[NP], x1[NP], l0[LO ? NP : 1], l1[LO ? NP : 1];
+
+    __device__ void fetch(const in_t *base, int64_t st, int t0, int T) {
+        const __amdgpu_buffer_rsrc_t r = rows_rsrc(base, (uint32_t)(T * st * sizeof(in_t)));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                *(uint32_t *)&tr[(8 * cc + 2 * e) * PT + r0] = (x0[e] & 0xffffu) | (x1[e] << 16);
-                *(uint32_t *)&tr[(8 * cc + 2 * e + 1) * PT + r0] = (x0[e] >> 16) | (x1[e] & 0xffff0000u);
+        for (int i = 0; i < NP; ++i) {
+            const int pi = min((int)threadIdx.x + NT * i, NPIECE - 1);  // extra threads repeat the last piece
+            const int rp = pi / (W / 8), cc = pi % (W / 8);
+            const uint32_t off = (uint32_t)(((t0 + 2 * rp) * st + 8 * cc) * sizeof(in_t));
+            const uint32_t off1 = off + (uint32_t)(st * sizeof(in_t));
+            if constexpr (LO) {
+                x0[i] = bload_op8<DT>(r, off, &l0[i]);
+                x1[i] = bload_op8<DT>(r, off1, &l1[i]);
+            } else {
+                x0[i] = bload16(r, off);
+                x1[i] = bload16(r, off1);
             }
         }
     }
-}
+    template <int PR, int PT, bool ROW, bool TR>
+    __device__ void put(uint16_t *row, uint16_t *tr, uint16_t *lo) const {
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int pi = threadIdx.x + NT * i;
+            if (pi >= NPIECE) continue;
+            const int rp = pi / (W / 8), cc = pi % (W / 8);
+            const int r0 = 2 * rp;
+            if constexpr (ROW) {
+                *(u32x4 *)&row[r0 * PR + 8 * cc] = x0[i];
+                *(u32x4 *)&row[(r0 + 1) * PR + 8 * cc] = x1[i];
+            }
+            if constexpr (LO && ROW) {
+                *(u32x4 *)&lo[r0 * PR + 8 * cc] = l0[i];
+                *(u32x4 *)&lo[(r0 + 1) * PR + 8 * cc] = l1[i];
+            }
+            if constexpr (TR) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    *(uint32_t *)&tr[(8 * cc + 2 * e) * PT + r0] = __builtin_amdgcn_perm(x1[i][e], x0[i][e], 0x05040100u);
+                    *(uint32_t *)&tr[(8 * cc + 2 * e + 1) * PT + r0] = __builtin_amdgcn_perm(x1[i][e], x0[i][e], 0x07060302u);
+                }
+            }
+        }
+    }
+};
 
 // A operand of a k-step of 16 along the permuted index of a C-layout tile:
 // lane reads entries [16ks + 4hi .. +3] and [16ks + 8 + 4hi .. +3] of its row.
@@ -91,12 +115,13 @@ __global__ __launch_bounds__(NT, 1) void attn_bwd_dkdv_kernel(AttnBwdK a) {
     constexpr int RB = (R + 31) / 32;  // 32-row blocks of dK^T
     constexpr int PQ = R + 8, PO = D + 8, PT = BQ + 4;
     constexpr bool SPL = DT == HOFA_F32;
-    __shared__ __attribute__((aligned(16))) uint16_t sQ[BQ * PQ];
-    __shared__ __attribute__((aligned(16))) uint16_t sQlo[SPL ? BQ * PQ : 8];
-    __shared__ __attribute__((aligned(16))) uint16_t sQt[RB * 32 * PT];
-    __shared__ __attribute__((aligned(16))) uint16_t sO[BQ * PO];
-    __shared__ __attribute__((aligned(16))) uint16_t sOt[D * PT];
-    __shared__ float sL[BQ], sD[BQ];
+    __shared__ __attribute__((aligned(16))) uint16_t sQ[2][BQ * PQ];
+    __shared__ __attribute__((aligned(16))) uint16_t sQlo[2][SPL ? BQ * PQ : 8];
+    __shared__ __attribute__((aligned(16))) uint16_t sQt[2][RB * 32 * PT];
+    __shared__ __attribute__((aligned(16))) uint16_t sO[2][BQ * PO];
+    __shared__ __attribute__((aligned(16))) uint16_t sOt[2][D * PT];
+    __shared__ __attribute__((aligned(16))) float sL[2][BQ];
+    __shared__ __attribute__((aligned(16))) float sD[2][BQ];
 
     const int nkb = (a.T + BKB - 1) / BKB;
     int bh, kblk;
@@ -129,7 +154,7 @@ __global__ __launch_bounds__(NT, 1) void attn_bwd_dkdv_kernel(AttnBwdK a) {
     for (int ks = 0; ks < DKS; ++ks)
         vop[ks] = key < a.T ? load_op8<DT>(vp + (int64_t)key * a.v_st + 16 * ks + 8 * hi) : u32x4{0, 0, 0, 0};
     // rows R..32*RB-1 of Q^T stay zero
-    for (int i = tid; i < RB * 32 * PT; i += NT) sQt[i] = 0;
+    for (int i = tid; i < 2 * RB * 32 * PT; i += NT) (&sQt[0][0])[i] = 0;
 
     f32x16 dvt[MB], dkt[RB];
 #pragma unroll
@@ -141,60 +166,85 @@ __global__ __launch_bounds__(NT, 1) void attn_bwd_dkdv_kernel(AttnBwdK a) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) dkt[rb][v] = 0.f;
 
-    for (int q0 = k0; q0 < a.T; q0 += BQ) {
-        __syncthreads();  // previous tile consumed
-        stage_rows<DT, R, PQ, PT, true, true, SPL>(qp, a.q_st, q0, a.T, sQ, sQt, sQlo);
-        stage_rows<DT, D, PO, PT, true, true>(op, a.o_st, q0, a.T, sO, sOt);
-        for (int i = tid; i < BQ; i += NT) {
-            sL[i] = q0 + i < a.T ? lse[q0 + i] : 0.f;
-            sD[i] = q0 + i < a.T ? dtp[q0 + i] : 0.f;
+    RowStage<DT, R> stq;
+    RowStage<DT, D> sto;
+    float ls = 0.f, ds = 0.f;
+    auto fetch = [&](int q0) {
+        stq.fetch(qp, a.q_st, q0, a.T);
+        sto.fetch(op, a.o_st, q0, a.T);
+        if (tid < BQ) {
+            ls = q0 + tid < a.T ? lse[q0 + tid] : 0.f;
+            ds = q0 + tid < a.T ? dtp[q0 + tid] : 0.f;
         }
-        __syncthreads();
-        if (q0 + BQ - 1 < kw0) continue;  // every query of the tile precedes this wave's keys
+    };
+    auto put = [&](int buf) {
+        stq.template put<PQ, PT, true, true>(sQ[buf], sQt[buf], sQlo[buf]);
+        sto.template put<PO, PT, true, true>(sO[buf], sOt[buf], nullptr);
+        if (tid < BQ) {
+            sL[buf][tid] = ls;
+            sD[buf][tid] = ds;
+        }
+    };
+    fetch(k0);
+    __syncthreads();  // pad rows of Q^T cleared
+    put(0);
+    __syncthreads();
+    int buf = 0;
+    for (int q0 = k0; q0 < a.T; q0 += BQ, buf ^= 1) {
+        const bool more = q0 + BQ < a.T;
+        if (more) fetch(q0 + BQ);
+        if (q0 + BQ - 1 >= kw0) {  // some query of the tile sees this wave's keys
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            f32x16 s, dp;
+            for (int qb = 0; qb < 2; ++qb) {
+                f32x16 s = {}, dp = {};
+                const uint16_t *qrow = &sQ[buf][(32 * qb + (lane & 31)) * PQ];
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                s[v] = 0.f;
-                dp[v] = 0.f;
-            }
-            const uint16_t *qrow = &sQ[(32 * qb + (lane & 31)) * PQ];
+                for (int ks = 0; ks < KS; ++ks) {
+                    const u32x4 qa = *(const u32x4 *)(qrow + 16 * ks + 8 * hi);
+                    s = mfma32<DT>(qa, kop[ks], s);
+                    if constexpr (SPL) {
+                        s = mfma32<DT>(qa, klo[ks], s);
+                        s = mfma32<DT>(*(const u32x4 *)(&sQlo[buf][(32 * qb + (lane & 31)) * PQ] + 16 * ks + 8 * hi),
+                                       kop[ks], s);
+                    }
+                }
+                const uint16_t *orow = &sO[buf][(32 * qb + (lane & 31)) * PO];
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const u32x4 qa = *(const u32x4 *)(qrow + 16 * ks + 8 * hi);
-                s = mfma32<DT>(qa, kop[ks], s);
-                if constexpr (SPL) {
-                    s = mfma32<DT>(qa, klo[ks], s);
-                    s = mfma32<DT>(*(const u32x4 *)(&sQlo[(32 * qb + (lane & 31)) * PQ] + 16 * ks + 8 * hi), kop[ks], s);
+                for (int ks = 0; ks < DKS; ++ks) dp = mfma32<DT>(*(const u32x4 *)(orow + 16 * ks + 8 * hi), vop[ks], dp);
+                // P and dS in place (C[query, key]: lane = key, v -> query)
+                const bool edge = q0 + 32 * qb < kw0 + 31 || q0 + 32 * qb + 31 >= a.T || kw0 + 31 >= a.T;
+                // query offsets 8g + e of this lane (g = v/4, e = v%4) are visible iff vlo <= 8g + e <= vhi
+                const int vlo = key - q0 - 32 * qb - 4 * hi;
+                const int vhi = key < a.T ? a.T - 1 - q0 - 32 * qb - 4 * hi : -1;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 lq = *(const f32x4 *)&sL[buf][32 * qb + 8 * g + 4 * hi];
+                    const f32x4 dq = *(const f32x4 *)&sD[buf][32 * qb + 8 * g + 4 * hi];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int v = 4 * g + e;
+                        float p = fast_exp2(fmaf(s[v], a.c, -lq[e]));
+                        if (edge) p = (8 * g + e >= vlo && 8 * g + e <= vhi) ? p : 0.f;
+                        s[v] = p;
+                        dp[v] = p * (dp[v] - dq[e]);
+                    }
+                }
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2) {
+                    const int ks4 = 2 * qb + k2;
+                    const u32x4 pb = pack8<DT>(s, 8 * k2);
+                    const u32x4 db = pack8<DT>(dp, 8 * k2);
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb)
+                        dvt[mb] = mfma32<DT>(perm_a(&sOt[buf][(32 * mb + (lane & 31)) * PT], ks4, hi), pb, dvt[mb]);
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+                        dkt[rb] = mfma32<DT>(perm_a(&sQt[buf][(32 * rb + (lane & 31)) * PT], ks4, hi), db, dkt[rb]);
                 }
             }
-            const uint16_t *orow = &sO[(32 * qb + (lane & 31)) * PO];
-#pragma unroll
-            for (int ks = 0; ks < DKS; ++ks) dp = mfma32<DT>(*(const u32x4 *)(orow + 16 * ks + 8 * hi), vop[ks], dp);
-            // P and dS in place (C[query, key]: lane = key, v -> query)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int qi = 32 * qb + 8 * (v / 4) + 4 * hi + (v % 4);
-                const int qq = q0 + qi;
-                float p = fast_exp2(fmaf(s[v], a.c, -sL[qi]));
-                if (qq < key || qq >= a.T || key >= a.T) p = 0.f;
-                s[v] = p;
-                dp[v] = p * (dp[v] - sD[qi]);
-            }
-#pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) {
-                const int ks4 = 2 * qb + k2;
-                const u32x4 pb = pack8<DT>(s, 8 * k2);
-                const u32x4 db = pack8<DT>(dp, 8 * k2);
-#pragma unroll
-                for (int mb = 0; mb < MB; ++mb)
-                    dvt[mb] = mfma32<DT>(perm_a(&sOt[(32 * mb + (lane & 31)) * PT], ks4, hi), pb, dvt[mb]);
-#pragma unroll
-                for (int rb = 0; rb < RB; ++rb)
-                    dkt[rb] = mfma32<DT>(perm_a(&sQt[(32 * rb + (lane & 31)) * PT], ks4, hi), db, dkt[rb]);
-            }
         }
+        if (more) put(buf ^ 1);
+        __syncthreads();
     }
     if (key >= a.T) return;
     // dV^T / dK^T: lane = key, rows 8(v/4) + 4hi + v%4 of each 32-row block
@@ -225,10 +275,10 @@ __global__ __launch_bounds__(NT, 1) void attn_bwd_dq_kernel(AttnBwdK a) {
     constexpr int RB = (R + 31) / 32;
     constexpr int PK = R + 8, PV = D + 8, PT = BN + 4;
     constexpr bool SPL = DT == HOFA_F32;
-    __shared__ __attribute__((aligned(16))) uint16_t sK[BN * PK];
-    __shared__ __attribute__((aligned(16))) uint16_t sKlo[SPL ? BN * PK : 8];
-    __shared__ __attribute__((aligned(16))) uint16_t sKt[RB * 32 * PT];
-    __shared__ __attribute__((aligned(16))) uint16_t sV[BN * PV];
+    __shared__ __attribute__((aligned(16))) uint16_t sK[2][BN * PK];
+    __shared__ __attribute__((aligned(16))) uint16_t sKlo[2][SPL ? BN * PK : 8];
+    __shared__ __attribute__((aligned(16))) uint16_t sKt[2][RB * 32 * PT];
+    __shared__ __attribute__((aligned(16))) uint16_t sV[2][BN * PV];
 
     const int nq = (a.T + BM - 1) / BM;
     int bh, qb;
@@ -256,7 +306,7 @@ __global__ __launch_bounds__(NT, 1) void attn_bwd_dq_kernel(AttnBwdK a) {
         oop[ks] = qrow < a.T ? load_op8<DT>(op + (int64_t)qrow * a.o_st + 16 * ks + 8 * hi) : u32x4{0, 0, 0, 0};
     const float lq = qrow < a.T ? a.lse[(int64_t)bh * a.T + qrow] : 0.f;
     const float dq_t = qrow < a.T ? a.dt[(int64_t)bh * a.T + qrow] : 0.f;
-    for (int i = tid; i < RB * 32 * PT; i += NT) sKt[i] = 0;
+    for (int i = tid; i < 2 * RB * 32 * PT; i += NT) (&sKt[0][0])[i] = 0;
 
     f32x16 dqt[RB];
 #pragma unroll
@@ -264,49 +314,62 @@ __global__ __launch_bounds__(NT, 1) void attn_bwd_dq_kernel(AttnBwdK a) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) dqt[rb][v] = 0.f;
 
+    RowStage<DT, R> stk;
+    RowStage<DT, D> stv;
     const int kend = min(a.T, q0 + BM);
-    for (int k0 = 0; k0 < kend; k0 += BN) {
-        __syncthreads();
-        stage_rows<DT, R, PK, PT, true, true, SPL>(kp, a.k_st, k0, a.T, sK, sKt, sKlo);
-        stage_rows<DT, D, PV, PT, true, false>(vp, a.v_st, k0, a.T, sV, nullptr);
-        __syncthreads();
-        if (k0 > qw0 + 31) continue;
+    stk.fetch(kp, a.k_st, 0, a.T);
+    stv.fetch(vp, a.v_st, 0, a.T);
+    __syncthreads();  // pad rows of K^T cleared
+    stk.template put<PK, PT, true, true>(sK[0], sKt[0], sKlo[0]);
+    stv.template put<PV, PT, true, false>(sV[0], nullptr, nullptr);
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = 0; k0 < kend; k0 += BN, buf ^= 1) {
+        const bool more = k0 + BN < kend;
+        if (more) {
+            stk.fetch(kp, a.k_st, k0 + BN, a.T);
+            stv.fetch(vp, a.v_st, k0 + BN, a.T);
+        }
+        if (k0 <= qw0 + 31) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            f32x16 s, dp;
+            for (int kb = 0; kb < 2; ++kb) {
+                f32x16 s = {}, dp = {};
+                const uint16_t *krow = &sK[buf][(32 * kb + (lane & 31)) * PK];
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                s[v] = 0.f;
-                dp[v] = 0.f;
-            }
-            const uint16_t *krow = &sK[(32 * kb + (lane & 31)) * PK];
+                for (int ks = 0; ks < KS; ++ks) {
+                    const u32x4 ka = *(const u32x4 *)(krow + 16 * ks + 8 * hi);
+                    s = mfma32<DT>(ka, qop[ks], s);
+                    if constexpr (SPL) {
+                        s = mfma32<DT>(ka, qlo[ks], s);
+                        s = mfma32<DT>(*(const u32x4 *)(&sKlo[buf][(32 * kb + (lane & 31)) * PK] + 16 * ks + 8 * hi),
+                                       qop[ks], s);
+                    }
+                }
+                const uint16_t *vrow = &sV[buf][(32 * kb + (lane & 31)) * PV];
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const u32x4 ka = *(const u32x4 *)(krow + 16 * ks + 8 * hi);
-                s = mfma32<DT>(ka, qop[ks], s);
-                if constexpr (SPL) {
-                    s = mfma32<DT>(ka, qlo[ks], s);
-                    s = mfma32<DT>(*(const u32x4 *)(&sKlo[(32 * kb + (lane & 31)) * PK] + 16 * ks + 8 * hi), qop[ks], s);
+                for (int ks = 0; ks < DKS; ++ks) dp = mfma32<DT>(*(const u32x4 *)(vrow + 16 * ks + 8 * hi), oop[ks], dp);
+                const bool edge = k0 + 32 * kb + 31 > qw0 || k0 + 32 * kb + 31 >= a.T;
+                const int lim = min(qrow, a.T - 1) - k0 - 32 * kb - 4 * hi;  // key offset visible iff <= lim
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    float p = fast_exp2(fmaf(s[v], a.c, -lq));
+                    if (edge) p = 8 * (v / 4) + (v % 4) <= lim ? p : 0.f;
+                    dp[v] = p * (dp[v] - dq_t);
+                }
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2) {
+                    const u32x4 db = pack8<DT>(dp, 8 * k2);
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb)
+                        dqt[rb] = mfma32<DT>(perm_a(&sKt[buf][(32 * rb + (lane & 31)) * PT], 2 * kb + k2, hi), db, dqt[rb]);
                 }
             }
-            const uint16_t *vrow = &sV[(32 * kb + (lane & 31)) * PV];
-#pragma unroll
-            for (int ks = 0; ks < DKS; ++ks) dp = mfma32<DT>(*(const u32x4 *)(vrow + 16 * ks + 8 * hi), oop[ks], dp);
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int kk = k0 + 32 * kb + 8 * (v / 4) + 4 * hi + (v % 4);
-                float p = fast_exp2(fmaf(s[v], a.c, -lq));
-                if (kk > qrow || kk >= a.T) p = 0.f;
-                dp[v] = p * (dp[v] - dq_t);
-            }
-#pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) {
-                const u32x4 db = pack8<DT>(dp, 8 * k2);
-#pragma unroll
-                for (int rb = 0; rb < RB; ++rb)
-                    dqt[rb] = mfma32<DT>(perm_a(&sKt[(32 * rb + (lane & 31)) * PT], 2 * kb + k2, hi), db, dqt[rb]);
-            }
         }
+        if (more) {
+            stk.template put<PK, PT, true, true>(sK[buf ^ 1], sKt[buf ^ 1], sKlo[buf ^ 1]);
+            stv.template put<PV, PT, true, false>(sV[buf ^ 1], nullptr, nullptr);
+        }
+        __syncthreads();
     }
     if (qrow >= a.T) return;
     in_t *dqr = (in_t *)a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)qrow * a.dq_st;
@@ -368,6 +431,9 @@ extern "C" int hofa_attn_bwd(const hofa_attn_bwd_args_t *a, void *stream) {
     const int es = elem_bytes(dt);
     for (const hofa_view_t *v : {&a->q, &a->k, &a->v, &a->dout, &a->dq, &a->dk, &a->dv})
         HOFA_REQUIRE(rows_ok(*v, es), HOFA_EINVAL, "hofa_attn_bwd: tensors need unit last stride and 16-byte aligned rows");
+    for (const hofa_view_t *v : {&a->q, &a->k, &a->v, &a->dout})
+        HOFA_REQUIRE((int64_t)(a->T + 2 * BKB) * v->stride[2] * es < (1ll << 31), HOFA_EUNSUPPORTED,
+                     "hofa_attn_bwd: one head's rows must span less than 2 GiB");
     AttnBwdK k{};
     k.q = a->q.data; k.k = a->k.data; k.v = a->v.data; k.dO = a->dout.data;
     k.lse = a->lse; k.dt = a->delta;

@@ -128,6 +128,40 @@ __device__ __forceinline__ u32x4 load_lo8_f32(const float *p) {
     return pack8<HOFA_BF16>(r);
 }
 
+// Range-checked loads through a buffer resource: an access at or past
+// `bytes` returns zeros, so tile loads past the last row need no branch.
+// `base` must be wave-uniform (derived from blockIdx and kernel arguments).
+constexpr int kBufRaw = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, bytes, kBufRaw);
+}
+
+__device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// 8 consecutive elements at byte offset `off` as a 16-bit operand quad; f32
+// inputs are rounded to bf16 (hi) and, when lo is given, their remainders.
+template <int DT>
+__device__ __forceinline__ u32x4 bload_op8(__amdgpu_buffer_rsrc_t r, uint32_t off, u32x4 *lo = nullptr) {
+    if constexpr (DT == HOFA_F32) {
+        const u32x4 a = bload16(r, off), b = bload16(r, off + 16);
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[e] = __uint_as_float(a[e]);
+            x[4 + e] = __uint_as_float(b[e]);
+        }
+        u32x4 hi, l;
+        split8<DT>(x, hi, l);
+        if (lo) *lo = l;
+        return hi;
+    } else {
+        return bload16(r, off);
+    }
+}
+
 // Block-index remap that keeps all blocks of one head on one XCD (blocks are
 // dispatched round-robin over 8 XCDs) and walks each head's row blocks from
 // the last to the first (longest causal rows first).
