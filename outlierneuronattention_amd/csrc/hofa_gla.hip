@@ -76,6 +76,7 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
     constexpr bool VLO = kRawSplit<DT>;  // f32/f16 inputs also split V
     __shared__ float sDec[Decay<J, GENERAL>::kFloats];
     __shared__ __attribute__((aligned(16))) uint16_t sVt[VLO ? 2 : 1][D * VP];
+    __shared__ __attribute__((aligned(16))) float sGs[D];
     if ((a.unsafe[blockIdx.x] != 0) != FB) return;  // the other launch handles this chunk
     const int bh = blockIdx.x / a.nc, c = blockIdx.x % a.nc;
     const int b = bh / a.H, h = bh % a.H, t0 = c * C;
@@ -83,6 +84,7 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
     load_decay<J, GENERAL, NT>(a, b, h, t0, dec);
     load_transposed<DT, D, VP, VLO, NT>((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, 0, t0, a.T, sVt[0],
                                     sVt[VLO ? 1 : 0], [](int, int) { return 1.f; });
+    for (int d = threadIdx.x; d < D; d += NT) sGs[d] = a.fuse ? load_any(a.gs, a.gs_dt, h * a.gs_sh + d * a.gs_sd) : 1.f;
     __syncthreads();
 
     const int lane = threadIdx.x & 63, hi = lane >> 5;
@@ -92,31 +94,15 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
 
     const in_t *qp = (const in_t *)a.q + b * a.q_sb + h * a.q_sh;
     const in_t *kp = (const in_t *)a.k + b * a.k_sb + h * a.k_sh;
+    const Rows<DT> qrows(qp, a.q_st, a.T), krows(kp, a.k_st, a.T);
     // 8 inlier channels 16ks + 8hi + e of row t, as floats (0 past T)
-    auto row8 = [&](const in_t *base, int64_t st, int t, int ks, float *x) {
-        if (t < a.T) {
-            const in_t *p = base + (int64_t)t * st + a.R + 16 * ks + 8 * hi;
-            if constexpr (DT == HOFA_F32) {
-                const f32x4 u = *(const f32x4 *)p, v = *(const f32x4 *)(p + 4);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    x[e] = u[e];
-                    x[4 + e] = v[e];
-                }
-            } else {
-                unpack16<DT>(*(const u32x4 *)p, x);
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = 0.f;
-        }
-    };
+    auto row8 = [&](const Rows<DT> &rows, int t, int ks, float *x) { rows.f8(t, a.R + 16 * ks + 8 * hi, x); };
     // Q~ = Q (.) exp(G): B operand (lane = query), hi + lo
     u32x4 qh[KS], ql[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         float x[8];
-        row8(qp, a.q_st, tq, ks, x);
+        row8(qrows, tq, ks, x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(dec.G(qi, 16 * ks + 8 * hi + e) * kLog2e);
         split8<OPB>(x, qh[ks], ql[ks]);
@@ -137,7 +123,7 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 float x[8];
-                row8(kp, a.k_st, t0 + kj, ks, x);
+                row8(krows, t0 + kj, ks, x);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(-dec.G(kj, 16 * ks + 8 * hi + e) * kLog2e);
                 u32x4 kh, kl;
@@ -219,15 +205,18 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) nr[32 * mb + 8 * (v / 4) + 4 * hi + (v % 4)] = from_f32<DT>(y[mb][v] * rs);
+                for (int g = 0; g < 4; ++g)
+                    store4<DT>(nr + 32 * mb + 8 * g + 4 * hi, y[mb][4 * g] * rs, y[mb][4 * g + 1] * rs,
+                               y[mb][4 * g + 2] * rs, y[mb][4 * g + 3] * rs);
             if (hi == 0) a.rstd[(int64_t)bh * a.T + tq] = rs;
         }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int dv = 32 * mb + 8 * (v / 4) + 4 * hi + (v % 4);
-                y[mb][v] *= f * load_any(a.gs, a.gs_dt, h * a.gs_sh + dv * a.gs_sd);
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 gs4 = *(const f32x4 *)&sGs[32 * mb + 8 * g + 4 * hi];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[mb][4 * g + e] *= f * gs4[e];
             }
     }
     if (tq >= a.T) return;
@@ -235,7 +224,8 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) yr[32 * mb + 8 * (v / 4) + 4 * hi + (v % 4)] = from_f32<DT>(y[mb][v]);
+        for (int g = 0; g < 4; ++g)
+            store4<DT>(yr + 32 * mb + 8 * g + 4 * hi, y[mb][4 * g], y[mb][4 * g + 1], y[mb][4 * g + 2], y[mb][4 * g + 3]);
 }
 
 // ------------------------------------------------------------------ host
@@ -284,6 +274,9 @@ int validate(const hofa_gla_fwd_args_t *a) {
     HOFA_REQUIRE(!a->fuse_norm_gate || (a->mix.data && a->gla_scale.data), HOFA_EINVAL,
                  "hofa_gla_fwd: fuse_norm_gate needs mix and gla_scale");
     HOFA_REQUIRE(a->state_out.dtype == HOFA_F32, HOFA_EINVAL, "hofa_gla_fwd: state_out must be float32");
+    for (const hofa_view_t *v : {&a->q, &a->k, &a->v})
+        HOFA_REQUIRE((int64_t)(a->T + 2 * C) * v->stride[2] * es < (1ll << 31), HOFA_EUNSUPPORTED,
+                     "hofa_gla_fwd: one head's q/k/v rows must span less than 2 GiB");
     HOFA_REQUIRE(!a->n_out.data || (a->fuse_norm_gate && a->rstd && a->n_out.dtype == dt && rows_ok(a->n_out, es)),
                  HOFA_EINVAL, "hofa_gla_fwd: n_out needs fuse_norm_gate, rstd, the dtype of y and aligned rows");
     return HOFA_OK;

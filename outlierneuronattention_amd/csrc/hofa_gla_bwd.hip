@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256) void gla_bwd_scan_kernel(GlaBwdK a) {
 // operands); FB = true: the others (element-wise intra-chunk terms).  Both
 // are launched over every chunk and leave at once for the chunks of the other.
 template <int DT, int D, int J, bool GENERAL, bool FB>
-__global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
+__global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
     using in_t = typename Stor<DT>::type;
     constexpr int TP = C + 4;             // token pitch of the transposed tiles
     constexpr int JB = (J + 31) / 32;     // 32-row channel blocks
@@ -267,6 +267,11 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
     auto qval = [&](int ti, int ch) { return t0 + ti < T ? to_f32<DT>(qp[(int64_t)(t0 + ti) * a.f.q_st + R + ch]) : 0.f; };
     auto kval = [&](int ti, int ch) { return t0 + ti < T ? to_f32<DT>(kp[(int64_t)(t0 + ti) * a.f.k_st + R + ch]) : 0.f; };
     const u32x4 zero4 = {0, 0, 0, 0};
+    const Rows<DT> qrows(qp, a.f.q_st, T), krows(kp, a.f.k_st, T), vrows(vp, a.f.v_st, T), drows(dop, D, T);
+    // K~ / Q~ (= k e^-G / q e^G) at (channel, chunk token) from the staged operands
+    auto staged = [&](int which, int ch, int tk) {
+        return op_to_f32<OPB>(sQK[which][0][ch * TP + tk]) + op_to_f32<OPB>(sQK[which][1][ch * TP + tk]);
+    };
 
     f32x16 acc[JB];  // dk^T (key side) or dq^T (query side): rows = channel, col = token
 #pragma unroll
@@ -287,15 +292,14 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
         u32x4 vh[DKS], vl[DKS];
 #pragma unroll
         for (int ks = 0; ks < DKS; ++ks) {
-            vh[ks] = vl[ks] = zero4;
-            if (ts < T) raw_op8<DT>(vp + (int64_t)ts * a.f.v_st + 16 * ks + 8 * hi, vh[ks], vl[ks]);
+            vrows.op8(ts, 16 * ks + 8 * hi, vh[ks], vl[ks]);
         }
         u32x4 kth[KS], ktl[KS];  // K~ = k e^-G of this key
         if constexpr (safe) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 float x[8];
-                row8f<DT>(kp, a.f.k_st, ts, T, R + 16 * ks + 8 * hi, x);
+                krows.f8(ts, R + 16 * ks + 8 * hi, x);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(-dec.G(s, 16 * ks + 8 * hi + e) * kLog2e);
                 split8<OPB>(x, kth[ks], ktl[ks]);
@@ -312,8 +316,8 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
             // M[t, s] = sum_d dO[t, d] V[s, d]
 #pragma unroll
             for (int ks = 0; ks < DKS; ++ks) {
-                u32x4 oh = zero4, ol = zero4;
-                if (t0 + tr < T) raw_op8<DT>(dop + (int64_t)(t0 + tr) * D + 16 * ks + 8 * hi, oh, ol);
+                u32x4 oh, ol;
+                drows.op8(t0 + tr, 16 * ks + 8 * hi, oh, ol);
                 mt = mfma32<OPB>(oh, vh[ks], mt);
                 if constexpr (SPL) {
                     mt = mfma32<OPB>(oh, vl[ks], mt);
@@ -325,7 +329,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
                     float x[8];
-                    row8f<DT>(qp, a.f.q_st, t0 + tr, T, R + 16 * ks + 8 * hi, x);
+                    qrows.f8(t0 + tr, R + 16 * ks + 8 * hi, x);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(dec.G(tr, 16 * ks + 8 * hi + e) * kLog2e);
                     u32x4 qh, ql;
@@ -398,23 +402,15 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
                     }
             }
         }
-        if constexpr (safe) {
+        in_t *dkr = (in_t *)a.dk + b * a.dk_sb + h * a.dk_sh + (int64_t)ts * a.dk_st + R;
+        in_t *dvr = (in_t *)a.dv + b * a.dv_sb + h * a.dv_sh + (int64_t)ts * a.dv_st;
+        // dk = e^-G (intra + e^G_last X) (factored) or intra + e^(G_last - G) X (element-wise),
+        // X = sum_d dH_end[c, d] V[s, d]; acc then holds this key's part of dGamma, -k dk
 #pragma unroll
-            for (int jb = 0; jb < JB; ++jb)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int ch = 32 * jb + crow(v, hi);
-                    acc[jb][v] = ch < J ? acc[jb][v] * fast_exp2(-dec.G(s, ch) * kLog2e) : 0.f;
-                }
-        }
-        if (c < nc - 1) {  // state gradient from later chunks
-            // dk^T[c, s] += e^(G_last,c - G_sc) sum_d dH_end[c, d] V[s, d]
-#pragma unroll
-            for (int jb = 0; jb < JB; ++jb) {
-                const int cr = 32 * jb + l32;
-                f32x16 x;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) x[v] = 0.f;
+        for (int jb = 0; jb < JB; ++jb) {
+            const int cr = 32 * jb + l32;
+            f32x16 x = {};
+            if (c < nc - 1) {
 #pragma unroll
                 for (int ks = 0; ks < DKS; ++ks) {
                     const int off = cr * D + 16 * ks + 8 * hi;
@@ -424,17 +420,36 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
                     x = mfma32<OPB>(sl, vh[ks], x);
                     if constexpr (SPL) x = mfma32<OPB>(sh, vl[ks], x);
                 }
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int ch = 32 * jb + crow(v, hi);
-                    if (ch < J) acc[jb][v] = fmaf(fast_exp2((dec.last(ch) - dec.G(s, ch)) * kLog2e), x[v], acc[jb][v]);
-                }
             }
-            // dv^T[d, s] += sum_c dH_end^T[d, c] K^[s, c]
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int ch0 = 32 * jb + 8 * g + 4 * hi;
+                if (ch0 >= J) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[jb][4 * g + e] = 0.f;
+                    continue;
+                }
+                float dk4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int v = 4 * g + e, ch = ch0 + e;
+                    if constexpr (safe) {
+                        const float y = fmaf(fast_exp2(dec.last(ch) * kLog2e), x[v], acc[jb][v]);
+                        dk4[e] = y * fast_exp2(-dec.G(s, ch) * kLog2e);
+                        acc[jb][v] = -staged(1, ch, s) * y;
+                    } else {
+                        dk4[e] = fmaf(fast_exp2((dec.last(ch) - dec.G(s, ch)) * kLog2e), x[v], acc[jb][v]);
+                        acc[jb][v] = -kval(s, ch) * dk4[e];
+                    }
+                }
+                if (ts < T) store4<DT>(dkr + ch0, dk4[0], dk4[1], dk4[2], dk4[3]);
+            }
+        }
+        if (c < nc - 1) {  // dv^T[d, s] += sum_c dH_end^T[d, c] K^[s, c]
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 float x[8];
-                row8f<DT>(kp, a.f.k_st, ts, T, R + 16 * ks + 8 * hi, x);
+                krows.f8(ts, R + 16 * ks + 8 * hi, x);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int ch = 16 * ks + 8 * hi + e;
@@ -453,19 +468,12 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
             }
         }
         if (ts < T) {
-            in_t *dkr = (in_t *)a.dk + b * a.dk_sb + h * a.dk_sh + (int64_t)ts * a.dk_st + R;
-            in_t *dvr = (in_t *)a.dv + b * a.dv_sb + h * a.dv_sh + (int64_t)ts * a.dv_st;
-#pragma unroll
-            for (int jb = 0; jb < JB; ++jb)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int ch = 32 * jb + crow(v, hi);
-                    if (ch < J) dkr[ch] = from_f32<DT>(acc[jb][v]);
-                }
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) dvr[32 * mb + crow(v, hi)] = from_f32<DT>(dvt[mb][v]);
+                for (int g = 0; g < 4; ++g)
+                    store4<DT>(dvr + 32 * mb + 8 * g + 4 * hi, dvt[mb][4 * g], dvt[mb][4 * g + 1], dvt[mb][4 * g + 2],
+                               dvt[mb][4 * g + 3]);
         }
     } else {
         // ================= query side: queries t = 32(w-2) + l32
@@ -474,8 +482,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
         u32x4 dh[DKS], dl[DKS];
 #pragma unroll
         for (int ks = 0; ks < DKS; ++ks) {
-            dh[ks] = dl[ks] = zero4;
-            if (tq < T) raw_op8<DT>(dop + (int64_t)tq * D + 16 * ks + 8 * hi, dh[ks], dl[ks]);
+            drows.op8(tq, 16 * ks + 8 * hi, dh[ks], dl[ks]);
         }
         for (int sb = 0; sb <= qb; ++sb) {
             const int sr = 32 * sb + l32;  // A-operand row (key) of this lane
@@ -485,8 +492,8 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
             // M^T[s, t] = sum_d V[s, d] dO[t, d]
 #pragma unroll
             for (int ks = 0; ks < DKS; ++ks) {
-                u32x4 va = zero4, vla = zero4;
-                if (t0 + sr < T) raw_op8<DT>(vp + (int64_t)(t0 + sr) * a.f.v_st + 16 * ks + 8 * hi, va, vla);
+                u32x4 va, vla;
+                vrows.op8(t0 + sr, 16 * ks + 8 * hi, va, vla);
                 mt = mfma32<OPB>(va, dh[ks], mt);
                 if constexpr (SPL) {
                     mt = mfma32<OPB>(va, dl[ks], mt);
@@ -550,22 +557,33 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
                     if constexpr (SPL) x = mfma32<OPB>(sh, dl[ks], x);
                 }
             }
+            // dq = e^G (intra + X) (factored) or intra + e^G X (element-wise); acc then holds q dq
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int ch = 32 * jb + crow(v, hi);
-                const float eg = ch < J ? fast_exp2(dec.G(t, ch) * kLog2e) : 0.f;
-                acc[jb][v] = safe ? eg * (acc[jb][v] + x[v]) : fmaf(eg, x[v], acc[jb][v]);
-            }
-        }
-        if (tq < T) {
-            in_t *dqr = (in_t *)a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)tq * a.dq_st + R;
+            for (int g = 0; g < 4; ++g) {
+                const int ch0 = 32 * jb + 8 * g + 4 * hi;
+                if (ch0 >= J) {
 #pragma unroll
-            for (int jb = 0; jb < JB; ++jb)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int ch = 32 * jb + crow(v, hi);
-                    if (ch < J) dqr[ch] = from_f32<DT>(acc[jb][v]);
+                    for (int e = 0; e < 4; ++e) acc[jb][4 * g + e] = 0.f;
+                    continue;
                 }
+                float dq4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int v = 4 * g + e, ch = ch0 + e;
+                    const float eg = fast_exp2(dec.G(t, ch) * kLog2e);
+                    if constexpr (safe) {
+                        const float y = acc[jb][v] + x[v];
+                        dq4[e] = eg * y;
+                        acc[jb][v] = staged(0, ch, t) * y;
+                    } else {
+                        dq4[e] = fmaf(eg, x[v], acc[jb][v]);
+                        acc[jb][v] = qval(t, ch) * dq4[e];
+                    }
+                }
+                if (tq < T)
+                    store4<DT>((in_t *)a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)tq * a.dq_st + R + ch0, dq4[0], dq4[1],
+                               dq4[2], dq4[3]);
+            }
         }
     }
 
@@ -578,7 +596,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int ch = 32 * jb + crow(v, hi);
-                if (ch < J) sDG[tok * DGP + ch] = qval(tok, ch) * acc[jb][v];
+                if (ch < J) sDG[tok * DGP + ch] = acc[jb][v];
             }
     }
     __syncthreads();
@@ -588,7 +606,7 @@ __global__ __launch_bounds__(NTB) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int ch = 32 * jb + crow(v, hi);
-                if (ch < J) sDG[tok * DGP + ch] -= kval(tok, ch) * acc[jb][v];
+                if (ch < J) sDG[tok * DGP + ch] += acc[jb][v];
             }
     }
     __syncthreads();
@@ -796,6 +814,10 @@ int validate(const hofa_gla_bwd_args_t *a) {
                      "hofa_gla_bwd: o and dout_attn need the dtype of q and aligned rows");
     }
     HOFA_REQUIRE((a->R * es) % 16 == 0, HOFA_EINVAL, "hofa_gla_bwd: the inlier columns must start 16-byte aligned");
+    for (const hofa_view_t *v : {&a->q, &a->k, &a->v})
+        HOFA_REQUIRE((int64_t)(a->T + 2 * C) * v->stride[2] * es < (1ll << 31) &&
+                         (int64_t)(a->T + 2 * C) * a->D * es < (1ll << 31),
+                     HOFA_EUNSUPPORTED, "hofa_gla_bwd: one head's rows must span less than 2 GiB");
     HOFA_REQUIRE(a->rstd && a->chunk_states && ((uintptr_t)a->chunk_states % 16) == 0, HOFA_EINVAL,
                  "hofa_gla_bwd: rstd and 16-byte aligned chunk_states from the forward are required");
     HOFA_REQUIRE(a->gla_scale.data && a->d_gla_scale.data, HOFA_EINVAL, "hofa_gla_bwd: gla_scale and d_gla_scale are required");

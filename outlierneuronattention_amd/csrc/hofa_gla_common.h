@@ -41,6 +41,55 @@ __device__ __forceinline__ void raw_op8(const typename Stor<DT>::type *p, u32x4 
     }
 }
 
+// The T rows of one head's [T, *] operand through a range-checked buffer:
+// rows at or past T read as zeros, so tile loads need no branches.  The
+// base pointer must be wave-uniform; the host checks that (T + 2C) rows span
+// less than 2 GiB.
+template <int DT>
+struct Rows {
+    using in_t = typename Stor<DT>::type;
+    __amdgpu_buffer_rsrc_t r;
+    int64_t st;
+    __device__ Rows(const in_t *base, int64_t row_stride, int T)
+        : r(rows_rsrc(base, (uint32_t)(T * row_stride * (int64_t)sizeof(in_t)))), st(row_stride) {}
+    __device__ uint32_t off(int row, int col) const { return (uint32_t)((row * st + col) * (int64_t)sizeof(in_t)); }
+    // 8 elements [col, col+8) of a row as floats
+    __device__ void f8(int row, int col, float *x) const {
+        const u32x4 a = bload16(r, off(row, col));
+        if constexpr (DT == HOFA_F32) {
+            const u32x4 b = bload16(r, off(row, col) + 16);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[e] = __uint_as_float(a[e]);
+                x[4 + e] = __uint_as_float(b[e]);
+            }
+        } else {
+            unpack16<DT>(a, x);
+        }
+    }
+    // 8 elements as a bf16 operand quad hi and the rounding remainder lo (zero for bf16)
+    __device__ void op8(int row, int col, u32x4 &hi, u32x4 &lo) const {
+        if constexpr (DT == HOFA_BF16) {
+            hi = bload16(r, off(row, col));
+            lo = u32x4{0, 0, 0, 0};
+        } else {
+            float x[8];
+            f8(row, col, x);
+            split8<HOFA_BF16>(x, hi, lo);
+        }
+    }
+};
+
+// Four consecutive outputs (16-byte aligned for f32, 8-byte for 16-bit types).
+template <int DT>
+__device__ __forceinline__ void store4(typename Stor<DT>::type *p, float a, float b, float c, float d) {
+    if constexpr (DT == HOFA_F32) {
+        *(f32x4 *)p = f32x4{a, b, c, d};
+    } else {
+        *(uint2 *)p = uint2{pack2<DT>(a, b), pack2<DT>(c, d)};
+    }
+}
+
 // Where a chunk kernel finds its inputs.  Forward and backward fill the
 // fields they use; strides are in elements.
 struct GlaK {
@@ -166,31 +215,15 @@ __device__ void load_decay(const GlaK &a, int b, int h, int t0, Decay<J, GENERAL
 template <int DT, int W, int PITCH, bool LO, int NTH, typename Scale>
 __device__ void load_transposed(const typename Stor<DT>::type *base, int64_t row_stride, int col0, int t0, int T,
                                 uint16_t *dst, uint16_t *dst_lo, Scale scale) {
-    using in_t = typename Stor<DT>::type;
     constexpr int NPIECE = (C / 2) * (W / 8);
+    const Rows<DT> rows(base, row_stride, T);
     for (int pi = threadIdx.x; pi < NPIECE; pi += NTH) {
         const int tp = pi / (W / 8), cc = pi % (W / 8);
         const int t = 2 * tp;
         float x[2][8];
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-            const int tt = t0 + t + r;
-            if (tt < T) {
-                const in_t *p = base + (int64_t)tt * row_stride + col0 + 8 * cc;
-                if constexpr (DT == HOFA_F32) {
-                    const f32x4 u = *(const f32x4 *)p, w = *(const f32x4 *)(p + 4);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        x[r][e] = u[e];
-                        x[r][4 + e] = w[e];
-                    }
-                } else {
-                    unpack16<DT>(*(const u32x4 *)p, x[r]);
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[r][e] = 0.f;
-            }
+            rows.f8(t0 + t + r, col0 + 8 * cc, x[r]);
 #pragma unroll
             for (int e = 0; e < 8; ++e) x[r][e] *= scale(t + r, 8 * cc + e);
         }
