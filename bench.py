@@ -232,9 +232,8 @@ def make_train_inputs(gen, dev="cuda"):
     B, T, H, D, R = T_B, T_T, T_H, T_D, T_R
     J = D - R
     x = torch.randn(B, T, H, 3 * D, generator=gen).to(dev, torch.bfloat16)
-    q, k, v = (x[..., i * D:(i + 1) * D].transpose(1, 2) for i in range(3))
-    q_o = q[..., :R]
-    k_o = k[..., :R]
+    # contiguous [B,H,T,d] leaves: the core's gradients are then stored as they are (no layout copies)
+    q, k, v = (x[..., i * D:(i + 1) * D].transpose(1, 2).contiguous() for i in range(3))
     lg = torch.full((B, H, T), -1.0, device=dev)
     la = torch.log(-F.logsigmoid(2 + 4 * torch.rand(1, H, 1, J, generator=gen))).to(dev)
     mix = torch.sigmoid(torch.randn(B, H, T, generator=gen)).to(dev)
@@ -252,6 +251,8 @@ def _train_step(inp, dy, backward=True):
     y = hofa_core(None, None, q, k, inp["v"], inp["lg"], inp["la"], inp["mix"], inp["gs"], T_R,
                   math.sqrt(T_D / T_R))  # outlier channels = q[..., :r], k[..., :r] (RoPE is outside the core)
     if backward:
+        for t in inp.values():
+            t.grad = None
         y.backward(dy)
     return y
 

@@ -17,9 +17,8 @@
 // so the row max and the rescale of O never leave a lane pair.  The rescale
 // is lazy: the reference max moves only when a tile's max exceeds it by more
 // than kTau (log2 units), so P stays below 2^kTau and O is rarely rescaled.
-// K (row-major) and V^T tiles are double-buffered in LDS and staged through
-// two register slots, so a tile's global loads have two tile-iterations to
-// arrive before they are written to LDS.
+// K (row-major) and V^T tiles are double-buffered in LDS; the next tile's
+// range-checked buffer loads are in flight while the current tile is consumed.
 #include "hofa_mfma.h"
 
 namespace hofa {
@@ -41,7 +40,7 @@ struct AttnFwdK {
 };
 
 template <int DT, int R, int D>
-__global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnFwdK a) {
+__global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_kernel(AttnFwdK a) {
     using in_t = typename Stor<DT>::type;
     constexpr int KS = R / 16;       // MFMA k-steps of S^T
     constexpr int MB = D / 32;       // 32-row blocks of O^T
@@ -83,10 +82,10 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnFwdK a) {
     const int kend = min(a.T, q0 + BM);
     const int ntiles = (kend + BN - 1) / BN;
 
-    // ---- cooperative tile loader (global -> registers -> LDS), two register
-    // slots so a tile's loads have two tile-iterations to arrive
-    u32x4 kreg[2][NKC], klo[2][NKC];
-    u32x4 vreg[2][NVP][2];
+    // ---- cooperative tile loader (global -> registers -> LDS): the next tile's
+    // loads are in flight while the current tile is consumed
+    u32x4 kreg[1][NKC], klo[1][NKC];
+    u32x4 vreg[1][NVP][2];
     constexpr int ES = sizeof(in_t);
     const __amdgpu_buffer_rsrc_t rk = rows_rsrc(kp, (uint32_t)(a.T * a.k_st * ES));
     const __amdgpu_buffer_rsrc_t rv = rows_rsrc(vp, (uint32_t)(a.T * a.v_st * ES));
@@ -214,21 +213,15 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnFwdK a) {
         }
     };
 
-    // tiles in pairs so the register slots are static: tile kt lives in LDS
-    // buffer kt%2 and register slot kt%2
+    // tile kt lives in LDS buffer kt%2
     gload(0, 0);
     lstore(0, 0);
-    if (ntiles > 1) gload(1, 1);
     __syncthreads();
-    for (int kt = 0; kt < ntiles; kt += 2) {
-        if (kt + 2 < ntiles) gload(kt + 2, 0);
-        tile(kt, 0);
-        if (kt + 1 < ntiles) lstore(1, 1);
-        __syncthreads();
-        if (kt + 1 >= ntiles) break;
-        if (kt + 3 < ntiles) gload(kt + 3, 1);
-        tile(kt + 1, 1);
-        if (kt + 2 < ntiles) lstore(0, 0);
+    for (int kt = 0; kt < ntiles; ++kt) {
+        const bool more = kt + 1 < ntiles;
+        if (more) gload(kt + 1, 0);
+        tile(kt, kt & 1);
+        if (more) lstore((kt + 1) & 1, 0);
         __syncthreads();
     }
 
@@ -245,13 +238,31 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnFwdK a) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int dv = 32 * mb + 8 * g + 4 * hi;
+            float ov[4], yv[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float ov = o[mb][4 * g + e] * inv;
-                float yv = mixv * ov;
-                if (a.accumulate) yv += to_f32<DT>(yr[dv + e]);
-                yr[dv + e] = from_f32<DT>(yv);
-                if (orow) orow[dv + e] = from_f32<DT>(ov);
+                ov[e] = o[mb][4 * g + e] * inv;
+                yv[e] = mixv * ov[e];
+            }
+            if (a.accumulate) {
+                if constexpr (DT == HOFA_F32) {
+                    const f32x4 p = *(const f32x4 *)(yr + dv);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) yv[e] += p[e];
+                } else {
+                    const uint2 p = *(const uint2 *)(yr + dv);
+                    yv[0] += to_f32<DT>((uint16_t)(p.x & 0xffffu));
+                    yv[1] += to_f32<DT>((uint16_t)(p.x >> 16));
+                    yv[2] += to_f32<DT>((uint16_t)(p.y & 0xffffu));
+                    yv[3] += to_f32<DT>((uint16_t)(p.y >> 16));
+                }
+            }
+            if constexpr (DT == HOFA_F32) {
+                *(f32x4 *)(yr + dv) = f32x4{yv[0], yv[1], yv[2], yv[3]};
+                if (orow) *(f32x4 *)(orow + dv) = f32x4{ov[0], ov[1], ov[2], ov[3]};
+            } else {
+                *(uint2 *)(yr + dv) = uint2{pack2<DT>(yv[0], yv[1]), pack2<DT>(yv[2], yv[3])};
+                if (orow) *(uint2 *)(orow + dv) = uint2{pack2<DT>(ov[0], ov[1]), pack2<DT>(ov[2], ov[3])};
             }
         }
     if (a.lse && hi == 0) a.lse[(int64_t)bh * a.T + qrow] = mref + __log2f(l);
