@@ -109,7 +109,8 @@ __device__ __forceinline__ u32x4 perm_a(const uint16_t *row, int ks, int hi) {
 }
 
 template <int DT, int R, int D>
-__global__ __launch_bounds__(NT, 1) void attn_bwd_dkdv_kernel(AttnBwdK a) {
+// Three waves per SIMD for the 16-bit d_h=64 kernels (LDS allows three blocks per CU).
+__global__ __launch_bounds__(NT, (DT != HOFA_F32 && D == 64 && R <= 32) ? 3 : 1) void attn_bwd_dkdv_kernel(AttnBwdK a) {
     using in_t = typename Stor<DT>::type;
     constexpr int KS = R / 16, DKS = D / 16, MB = D / 32;
     constexpr int RB = (R + 31) / 32;  // 32-row blocks of dK^T
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(NT, 1) void attn_bwd_dkdv_kernel(AttnBwdK a) {
 }
 
 template <int DT, int R, int D>
-__global__ __launch_bounds__(NT, 1) void attn_bwd_dq_kernel(AttnBwdK a) {
+__global__ __launch_bounds__(NT, (DT != HOFA_F32 && D == 64 && R <= 32) ? 4 : 1) void attn_bwd_dq_kernel(AttnBwdK a) {
     using in_t = typename Stor<DT>::type;
     constexpr int KS = R / 16, DKS = D / 16;
     constexpr int RB = (R + 31) / 32;
