@@ -285,6 +285,78 @@ def bench_train(steps: int, warmup: int):
                 timing="eager launches (autograd), HIP events on the current stream")
 
 
+# ---------------------------------------------------------------- full model (cfg5)
+M_LAYERS, M_D, M_H, M_R, M_VOCAB = 24, 1024, 16, 16, 50304
+
+
+def model_decode_bytes(model, B: int, L: int) -> int:
+    """Algorithmic HBM bytes of one greedy decode step at attended length L:
+    every layer's outlier caches (B*H*L*(r + d_h) bf16) and fp32 GLA state
+    (read and written), plus every parameter once (bf16)."""
+    n = 0
+    for layer in model.layers:
+        a = layer.attn
+        n += B * a.num_heads * L * (a.r + a.d_head) * 2 + B * a.num_heads * a.j * a.d_head * 4 * 2
+    return n + sum(p.numel() * p.element_size() for p in model.parameters())
+
+
+def model_prefill_flops(B: int, T: int) -> float:
+    """Algorithmic FLOPs of the cfg5 prefill: per layer the Q/K/V/out
+    projections and the 4x MLP (2*B*T*12*d^2), the causal outlier attention
+    (B*H*T^2*(r + d_h)) and the chunked GLA (6*B*H*T*j*d_h); the LM head on
+    the last row only (what generation needs)."""
+    dh = M_D // M_H
+    j = dh - M_R
+    per_layer = 2 * B * T * 12 * M_D * M_D + B * M_H * T * T * (M_R + dh) + 6 * B * M_H * T * j * dh
+    return M_LAYERS * per_layer + 2 * B * M_D * M_VOCAB
+
+
+def bench_model(B: int, prompt: int = 65536, steps: int = 256, warm: int = 4, seed: int = 5):
+    """cfg5: a 24-layer 350M-style SubwordLM (d_model 1024, H=16, d_h=64, r=16,
+    vocab 50304, bf16, random init from seed) prefills ``prompt`` random ids,
+    then decodes ``steps`` greedy tokens from captured HIP graphs
+    (outlierneuronattention_amd.decode_loop)."""
+    from outlierneuronattention_amd.config import ModelConfig
+    from outlierneuronattention_amd.decode_loop import GreedyGraphDecoder
+    from outlierneuronattention_amd.HybridOutlierFactorizedAttention import SubwordLM
+    torch.manual_seed(seed)
+    cfg = ModelConfig(d_model=M_D, num_heads=M_H, num_layers=M_LAYERS, r=M_R, device="cuda")
+    with torch.device("cuda"):
+        model = SubwordLM(M_VOCAB, cfg)
+    model = model.to(torch.bfloat16).eval()
+    gen = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, M_VOCAB, (B, prompt), generator=gen).to("cuda")
+    dec = GreedyGraphDecoder(model, B, prompt + warm + steps + 1)
+    with torch.no_grad():
+        dec.prefill(ids[:, :2048])  # warm-up (GEMM heuristics, workspaces)
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev[0].record()
+        dec.prefill(ids)
+        ev[1].record()
+        dec.decode(warm)          # eager step + graph capture + replays
+        torch.cuda.synchronize()
+        ev[2].record()
+        toks = dec.decode(steps)  # graph replays only
+        ev[3].record()
+        torch.cuda.synchronize()
+    pre_ms = ev[0].elapsed_time(ev[1])
+    dec_ms = ev[2].elapsed_time(ev[3]) / steps
+    L_mid = prompt + warm + steps // 2
+    nbytes = model_decode_bytes(model, B, L_mid)
+    fl = model_prefill_flops(B, prompt)
+    distinct = int(torch.unique(toks).numel())
+    del dec, model
+    torch.cuda.empty_cache()
+    return dict(B=B, prompt=prompt, steps=steps, prefill_ms=round(pre_ms, 2),
+                prefill_tok_per_s=round(B * prompt / pre_ms * 1e3, 1),
+                prefill_tflops=round(fl / (pre_ms * 1e-3) / 1e12, 1),
+                decode_ms_per_step=round(dec_ms, 4), decode_tok_per_s=round(B / dec_ms * 1e3, 1),
+                decode_bytes_per_step=nbytes, decode_gbs=round(nbytes / (dec_ms * 1e-3) / 1e9, 1),
+                decode_hbm_frac=round(nbytes / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                distinct_tokens=distinct)
+
+
 def cpu_baseline_decode(B: int, budget_s: float = 10.0):
     """Oracle decode step (torch CPU fp32) on the cfg3 shape: time until the
     budget is spent (at least 2 steps after one warm-up)."""
@@ -353,7 +425,7 @@ def main():
     ap.add_argument("--batch", type=int, default=4, help="batch of the headline decode line")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "train", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "train", "model", "copy"], default="all",
                     help="run one leg and print its result (profiling runs); default: the full line")
     ap.add_argument("--eager", action="store_true", help="decode with plain launches instead of graph replay")
     args = ap.parse_args()
@@ -372,6 +444,8 @@ def main():
             res = bench_prefill(max(5, min(50, args.steps // 20)), 3)
         elif args.only == "train":
             res = bench_train(max(5, min(20, args.steps // 50)), 3)
+        elif args.only == "model":
+            res = bench_model(args.batch)
         else:
             res = calibrate_copy()
         print(json.dumps({"only": args.only, "result": res}), flush=True)
@@ -383,6 +457,12 @@ def main():
     hot = bench_decode_hot(1, min(args.steps, 500))
     prefill = bench_prefill(max(5, min(50, args.steps // 20)), 3)
     train = bench_train(max(5, min(20, args.steps // 50)), 3)
+    model = {}
+    for mb in (1, 4):
+        try:
+            model[f"B{mb}"] = bench_model(mb)
+        except Exception as e:  # the headline line must still print
+            model[f"B{mb}"] = {"error": f"{type(e).__name__}: {e}"[:300]}
     cpu = None if args.skip_cpu else cpu_baseline_decode(args.batch, args.cpu_budget)
     achieved = head["gbs"]
     line = {
@@ -411,6 +491,9 @@ def main():
                    "B1_llc_resident": {k: round(v, 3) if isinstance(v, float) else v for k, v in hot.items()}},
         "prefill_fwd": prefill,
         "train_fwd_bwd": train,
+        "model_cfg5": dict(workload="cfg5: 24-layer SubwordLM (d_model 1024, H=16, d_h=64, r=16, vocab 50304, bf16, "
+                                    "random init), prefill 65536 random ids, then 256 greedy steps from captured "
+                                    "HIP graphs", **model),
     }
     print(json.dumps(line), flush=True)
 
