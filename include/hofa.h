@@ -260,6 +260,112 @@ typedef struct {
 size_t hofa_gla_bwd_workspace_bytes(const hofa_gla_bwd_args_t *args);
 int hofa_gla_bwd(const hofa_gla_bwd_args_t *args, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Single-token decode of a TransformerBlock: the work around hofa_decode.
+ *
+ * hofa_rows_linear: a row-batched linear for decode (B <= 4 rows),
+ *   xn      = LayerNorm(x; ln_w, ln_b, ln_eps) when ln_w is non-NULL, else x,
+ *             rounded to dtype (the output of nn.LayerNorm)
+ *   t       = round(xn[b] . w[n] + bias[n])            bias optional
+ *   t       = round(GELU_erf(t))                       act = 1
+ *   t       = round(t * scale)                         n < scale_cols
+ *   y[b, n] = round(res[b, n] + t)                     res optional, may alias y
+ * With argmax non-NULL it also folds max_n y[b, n] (first index on ties)
+ * into argmax[b] as a 64-bit key (order-preserving value bits << 32 |
+ * 0xffffffff - n) by atomic max; argmax[] must hold 0 before the call
+ * (hofa_decode_advance clears it).  Replaces, for one token, nn.LayerNorm +
+ * nn.Linear (+ nn.GELU) + the residual add of TransformerBlock.forward_step
+ * (src/HybridOutlierFactorizedAttention.py:447-451), the scaled W_q/W_k/W_v
+ * projections of forward_step (:223-235), out_proj, and SubwordLM.lm_head
+ * (:471) with the greedy argmax of src/inference.py:220-221.
+ * Rows are contiguous; x, ln_w, ln_b, w, bias, res and y share dtype
+ * (bf16 | f16).  w is [N, K] (nn.Linear layout), 16-byte aligned.
+ * Supported: 1 <= B <= 4, K a multiple of 8 and at most 4096.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    int32_t B, K, N, dtype;
+    int32_t act;
+    int32_t scale_cols;
+    float scale;
+    float ln_eps;
+    const void *x;
+    int64_t x_stride;
+    const void *ln_w, *ln_b;
+    const void *w;
+    const void *bias;
+    const void *res;
+    int64_t res_stride;
+    void *y;
+    int64_t y_stride;
+    unsigned long long *argmax;
+} hofa_rows_linear_args_t;
+
+int hofa_rows_linear(const hofa_rows_linear_args_t *args, void *stream);
+
+/*
+ * hofa_decode_prologue: per (b, h), from qkv = [B, 3*H*D] (Q | K | V of one
+ * token, Q and K already scaled by d_h^-1/4):
+ *   gate = round(Q . gate_w[h, :D] + K . gate_w[h, D:] + gate_b[h])
+ *   log_gamma[b, h] = round(logsigmoid(-gate))                       (f32 out)
+ *   mix[b, h] = round(sigmoid(round(Q . mix_w[h, :D] + K . mix_w[h, D:] + mix_b[h])))
+ *               or round(sigmoid(fixed_mix[h]))                      (f32 out)
+ *   Q[:R], K[:R] <- RoPE at row *pos of cos/sin [rope_rows, R] (in place in
+ *                   qkv; skipped when cos is NULL).  Tables are f32 (one
+ *                   rounding) or of the qkv dtype (rope_dtype; each product
+ *                   rounded, as a 16-bit module computes it)
+ *   cache_k[b, h, *pos, :] = K[:R],  cache_v[b, h, *pos, :] = V
+ * Replaces the gates, RoPE and cache append of forward_step
+ * (src/HybridOutlierFactorizedAttention.py:67-95, :365-387) with the
+ * position read on the device.  Caches are contiguous [B,H,cache_len,R] and
+ * [B,H,cache_len,D]; gate_w/mix_w [H, 2D]; everything shares dtype
+ * (bf16 | f16) except cos/sin, log_gamma/mix (f32) and pos (int64).
+ * Supported: D in {64, 128}, R even, 0 < R <= 64, R < D.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    int32_t B, H, D, R;
+    int32_t dtype;
+    int32_t cache_len;
+    int32_t rope_rows;
+    int32_t rope_dtype;
+    void *qkv;
+    int64_t qkv_stride;
+    const void *gate_w, *gate_b;
+    const void *mix_w, *mix_b;
+    const void *fixed_mix;
+    const void *cos, *sin;
+    const int64_t *pos;
+    void *cache_k, *cache_v;
+    float *log_gamma, *mix;
+} hofa_decode_prologue_args_t;
+
+int hofa_decode_prologue(const hofa_decode_prologue_args_t *args, void *stream);
+
+/*
+ * hofa_decode_advance: ends one greedy step.  For each batch row b the token
+ * idx = the index in argmax[b] (see hofa_rows_linear) is written to tok[b]
+ * and out[b, *col] (when *col < out_cols), and emb[idx, :] (the tied
+ * embedding, [vocab, d_model]) becomes x[b, :], the next step's input; then
+ * argmax[] is cleared and *col, *pos and *seq_len advance by one.  Replaces
+ * the greedy feedback of the generation loop (src/inference.py:220-239).
+ * Supported: 1 <= B <= 4; emb and x share dtype (bf16 | f16).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    int32_t B, d_model, vocab, dtype;
+    int32_t out_cols;
+    int32_t reserved;
+    unsigned long long *argmax;
+    const void *emb;
+    void *x;
+    int64_t x_stride;
+    int64_t *tok;
+    int64_t *out;
+    int64_t out_stride;
+    int64_t *col, *pos;
+    int32_t *seq_len;
+} hofa_decode_advance_args_t;
+
+int hofa_decode_advance(const hofa_decode_advance_args_t *args, void *stream);
+
 /* Library-wide helpers. */
 const char *hofa_last_error(void);
 int hofa_version(void);

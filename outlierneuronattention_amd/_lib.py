@@ -87,6 +87,41 @@ class GlaBwdArgs(ctypes.Structure):
                 ("dout_attn", View), ("delta", ctypes.c_void_p)]
 
 
+class RowsLinearArgs(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("K", ctypes.c_int32), ("N", ctypes.c_int32), ("dtype", ctypes.c_int32),
+                ("act", ctypes.c_int32), ("scale_cols", ctypes.c_int32),
+                ("scale", ctypes.c_float), ("ln_eps", ctypes.c_float),
+                ("x", ctypes.c_void_p), ("x_stride", ctypes.c_int64),
+                ("ln_w", ctypes.c_void_p), ("ln_b", ctypes.c_void_p),
+                ("w", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+                ("res", ctypes.c_void_p), ("res_stride", ctypes.c_int64),
+                ("y", ctypes.c_void_p), ("y_stride", ctypes.c_int64),
+                ("argmax", ctypes.c_void_p)]
+
+
+class DecodePrologueArgs(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("H", ctypes.c_int32), ("D", ctypes.c_int32), ("R", ctypes.c_int32),
+                ("dtype", ctypes.c_int32), ("cache_len", ctypes.c_int32), ("rope_rows", ctypes.c_int32),
+                ("rope_dtype", ctypes.c_int32),
+                ("qkv", ctypes.c_void_p), ("qkv_stride", ctypes.c_int64),
+                ("gate_w", ctypes.c_void_p), ("gate_b", ctypes.c_void_p),
+                ("mix_w", ctypes.c_void_p), ("mix_b", ctypes.c_void_p),
+                ("fixed_mix", ctypes.c_void_p),
+                ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p),
+                ("pos", ctypes.c_void_p),
+                ("cache_k", ctypes.c_void_p), ("cache_v", ctypes.c_void_p),
+                ("log_gamma", ctypes.c_void_p), ("mix", ctypes.c_void_p)]
+
+
+class DecodeAdvanceArgs(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("d_model", ctypes.c_int32), ("vocab", ctypes.c_int32),
+                ("dtype", ctypes.c_int32), ("out_cols", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("argmax", ctypes.c_void_p), ("emb", ctypes.c_void_p),
+                ("x", ctypes.c_void_p), ("x_stride", ctypes.c_int64),
+                ("tok", ctypes.c_void_p), ("out", ctypes.c_void_p), ("out_stride", ctypes.c_int64),
+                ("col", ctypes.c_void_p), ("pos", ctypes.c_void_p), ("seq_len", ctypes.c_void_p)]
+
+
 # (name, restype, argtypes) of every entry point declared in include/hofa.h
 EXPORTS = [
     ("hofa_decode_workspace_bytes", ctypes.c_size_t, [ctypes.POINTER(DecodeArgs)]),
@@ -99,6 +134,9 @@ EXPORTS = [
     ("hofa_attn_bwd", ctypes.c_int, [ctypes.POINTER(AttnBwdArgs), ctypes.c_void_p]),
     ("hofa_gla_bwd_workspace_bytes", ctypes.c_size_t, [ctypes.POINTER(GlaBwdArgs)]),
     ("hofa_gla_bwd", ctypes.c_int, [ctypes.POINTER(GlaBwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    ("hofa_rows_linear", ctypes.c_int, [ctypes.POINTER(RowsLinearArgs), ctypes.c_void_p]),
+    ("hofa_decode_prologue", ctypes.c_int, [ctypes.POINTER(DecodePrologueArgs), ctypes.c_void_p]),
+    ("hofa_decode_advance", ctypes.c_int, [ctypes.POINTER(DecodeAdvanceArgs), ctypes.c_void_p]),
     ("hofa_last_error", ctypes.c_char_p, []),
     ("hofa_version", ctypes.c_int, []),
 ]

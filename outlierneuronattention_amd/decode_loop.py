@@ -27,14 +27,26 @@ reverse, and replays alternate between them.
 
 Only the hybrid attention path (0 < r < d_head, no width-split heads) is
 supported, which is the configuration the reference's graph benchmark runs.
+
+For 16-bit models (bf16/f16, batch <= 4, d_model <= 1024) the step is the
+fused one (``fused=True``, the default there): per layer a LayerNorm+QKV
+row-linear, the gate/RoPE/cache-append prologue, the split-K decode, the
+out-projection with its residual, LayerNorm+fc1+GELU and fc2 with its
+residual (``decode_layer``), then LayerNorm+LM head with a device argmax and
+one kernel that feeds the token back -- about seven launches per layer.
+``fused=False`` keeps the module's own torch ops around the decode kernel.
 """
 from __future__ import annotations
+
+import ctypes
 
 import torch
 import torch.nn.functional as F
 
+from . import _lib
+from .decode_layer import decode_advance, decode_prologue, rows_linear
 from .HybridOutlierFactorizedAttention import SubwordLM
-from .hofa_decode import fused_hofa_decode
+from .hofa_decode import decode_args, fused_hofa_decode
 from .modules import apply_rotary_pos_emb
 
 
@@ -71,7 +83,7 @@ class GreedyGraphDecoder:
     states are allocated once, in the dtype of the model's parameters.
     """
 
-    def __init__(self, model: SubwordLM, batch: int, capacity: int):
+    def __init__(self, model: SubwordLM, batch: int, capacity: int, fused: bool | None = None):
         for layer in model.layers:
             a = layer.attn
             if not (0 < a.r < a.d_head) or a.forced_mha_heads > 0:
@@ -100,6 +112,29 @@ class GreedyGraphDecoder:
         self.n_prompt = 0
         self.n_done = 0
         self.parity = 0  # which state buffer holds the current state
+        d = model.ln_f.normalized_shape[0]
+        can_fuse = self.dtype in (torch.bfloat16, torch.float16) and batch <= 4 and 4 * d <= 4096
+        if fused and not can_fuse:
+            raise NotImplementedError("the fused decode step needs bf16/f16 weights, batch <= 4 and d_model <= 1024")
+        self.fused = can_fuse if fused is None else bool(fused)
+        if self.fused:
+            self._init_fused(d)
+
+    def _init_fused(self, d: int):
+        """Buffers of the fused step and a concatenated [3d, d] Q|K|V weight per layer."""
+        dev, dt, B = self.device, self.dtype, self.B
+        m = self.model
+        self.w_qkv = [torch.cat([layer.attn.W_q.weight, layer.attn.W_k.weight, layer.attn.W_v.weight]).contiguous()
+                      for layer in m.layers]
+        H = m.layers[0].attn.num_heads
+        self.x = torch.zeros(B, d, device=dev, dtype=dt)          # residual stream of the current token
+        self.qkv = torch.zeros(B, 3 * d, device=dev, dtype=dt)
+        self.y_attn = torch.zeros(B, H, 1, d // H, device=dev, dtype=dt)
+        self.h_mlp = torch.zeros(B, 4 * d, device=dev, dtype=dt)
+        self.lg = torch.zeros(B, H, device=dev, dtype=torch.float32)
+        self.mix = torch.zeros(B, H, device=dev, dtype=torch.float32)
+        self.keys = torch.zeros(B, dtype=torch.int64, device=dev)  # argmax keys (cleared by the advance kernel)
+        self.ws = None
 
     # ------------------------------------------------------------------ prefill
     @torch.no_grad()
@@ -127,6 +162,9 @@ class GreedyGraphDecoder:
         self.tok.copy_(logits.argmax(-1))
         self.logits = torch.empty_like(logits)
         self.logits.copy_(logits)
+        if self.fused:
+            self.x.copy_(m.token_emb(self.tok)[:, 0])
+            self.keys.zero_()
         self.graphs = None
         return logits
 
@@ -134,6 +172,8 @@ class GreedyGraphDecoder:
     def _step(self, parity: int):
         """One greedy token; graph-capturable (no host reads, no allocation
         outside the capture pool)."""
+        if self.fused:
+            return self._step_fused(parity)
         m = self.model
         x = m.token_emb(self.tok)
         for i, layer in enumerate(m.layers):
@@ -150,6 +190,47 @@ class GreedyGraphDecoder:
         self.pos.add_(1)
         self.seq_len.add_(1)
         self.col.add_(1)
+
+    def _step_fused(self, parity: int):
+        """The fused greedy step: seven launches per layer, then the LM head
+        with argmax and the feedback kernel; allocates nothing."""
+        m, B = self.model, self.B
+        x = self.x
+        for i, layer in enumerate(m.layers):
+            a = layer.attn
+            H, D = a.num_heads, a.d_head
+            HD = H * D
+            rows_linear(x, self.w_qkv[i], self.qkv, ln=(layer.ln_1.weight, layer.ln_1.bias, layer.ln_1.eps),
+                        scale=1.0 / D ** 0.25, scale_cols=2 * HD)
+            ck, cv = self.caches[i]
+            decode_prologue(a, self.qkv, ck, cv, self.pos, self.lg, self.mix)
+            q = self.qkv[:, :HD].view(B, H, 1, D)
+            k = self.qkv[:, HD:2 * HD].view(B, H, 1, D)
+            v = self.qkv[:, 2 * HD:].view(B, H, 1, D)
+            s_in, s_out = self.states[i][parity], self.states[i][1 - parity]
+            args, _, keep = decode_args(q, k, v, ck, cv, s_in, s_out, self.lg, self.mix, a.gla_scale.view(H, D),
+                                        a.r, ck.shape[2], (D / a.r) ** 0.5,
+                                        log_alpha=a.log_alpha if a.learnable_alpha else None,
+                                        seq_len_dev=self.seq_len, y=self.y_attn)
+            lib = _lib.load()
+            nbytes = lib.hofa_decode_workspace_bytes(ctypes.byref(args))
+            if nbytes == 0:
+                _lib.check(-1, "decode step")
+            if self.ws is None or self.ws.numel() < nbytes:
+                if torch.cuda.is_current_stream_capturing():
+                    raise RuntimeError("decode workspace must be sized before graph capture")
+                self.ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            _lib.check(lib.hofa_decode(ctypes.byref(args), self.ws.data_ptr(), self.ws.numel(),
+                                       _lib.stream_handle(self.device)), "decode step")
+            del keep
+            rows_linear(self.y_attn.view(B, HD), a.out_proj.weight, x, res=x)
+            fc1, fc2 = layer.mlp[0], layer.mlp[2]
+            rows_linear(x, fc1.weight, self.h_mlp, bias=fc1.bias, ln=(layer.ln_2.weight, layer.ln_2.bias,
+                                                                      layer.ln_2.eps), gelu=True)
+            rows_linear(self.h_mlp, fc2.weight, x, bias=fc2.bias, res=x)
+        rows_linear(x, m.lm_head.weight, self.logits[:, 0], ln=(m.ln_f.weight, m.ln_f.bias, m.ln_f.eps),
+                    argmax=self.keys)
+        decode_advance(self.keys, m.lm_head.weight, x, self.tok, self.out, self.col, self.pos, self.seq_len)
 
     @torch.no_grad()
     def decode(self, steps: int, graphs: bool = True) -> torch.Tensor:
