@@ -6,7 +6,7 @@
 // chunks of every head run in parallel and only an element-wise fp32 scan is
 // sequential over chunks:
 //
-//   1. gla_state_kernel   grid (B*H*nc), 2 waves: per chunk, in-chunk
+//   1. gla_state_kernel   grid (B*H*nc), 4 waves: per chunk, in-chunk
 //      inclusive cumsum G of the log decay (fp32, see Decay), then
 //        dS^T[D x J] = V_c^T (K_c (.) exp(G_last - G))        v_mfma_f32_16x16x32
 //      every exponent <= 0.  Writes dS^T and G_last.

@@ -238,7 +238,7 @@ __device__ void load_transposed(const typename Stor<DT>::type *base, int64_t row
     }
 }
 
-constexpr int kStateThreads = 128;
+constexpr int kStateThreads = 256;  // four waves: the LDS footprint allows four blocks per CU
 
 // Per chunk: in-chunk cumsum G of the log decay, then
 //   forward (BWD=false): out^T[D x J] = V_c^T (K_c (.) exp(G_last - G))
@@ -246,7 +246,7 @@ constexpr int kStateThreads = 128;
 // with the key operand read at columns [key_col0, key_col0+J) of a.k and the
 // value operand from a.v (every exponent <= 0).  Writes out^T to ws_ds and
 // G_last to ws_gl, and whether the chunk's decay range exceeds kSafeRange to
-// unsafe[].  2 waves, v_mfma_f32_16x16x32 tiles, hi/lo split operands.
+// unsafe[].  4 waves, v_mfma_f32_16x16x32 tiles, hi/lo split operands.
 template <int DT, int D, int J, bool GENERAL, bool BWD>
 __global__ __launch_bounds__(kStateThreads) void gla_state_kernel(GlaK a) {
     using in_t = typename Stor<DT>::type;
