@@ -10,7 +10,7 @@
 //      inclusive cumsum G of the log decay (fp32, see Decay), then
 //        dS^T[D x J] = V_c^T (K_c (.) exp(G_last - G))        v_mfma_f32_16x16x32
 //      every exponent <= 0.  Writes dS^T and G_last.
-//   2. gla_scan_kernel    grid (B*H, D*J/1024): S_in(c) = S, S <- exp(G_last) S + dS,
+//   2. gla_scan_kernel    grid (B*H, D/16): S_in(c) = S, S <- exp(G_last) S + dS,
 //      writes S_in(c) transposed as a hi/lo pair of 16-bit operands (and, for
 //      a backward pass, untransposed as a second pair) and the final fp32 state.
 //   3. gla_out_kernel     grid (B*H*nc), 2 waves x 32 query rows:
@@ -33,12 +33,21 @@ namespace {
 using namespace gla;
 constexpr int NT = 128;  // threads of the output kernel
 
+// One block per (head, 16 value rows): thread (dv, j4) carries S[j4..j4+3][dv]
+// in registers across the chunks.  Planes 0/1 (S^T, j contiguous) are stored
+// directly; planes 2/3 (S, d contiguous), written only for a backward pass,
+// go through a double-buffered LDS transpose so that both layouts leave with
+// contiguous stores.
+constexpr int kScanRows = 16;
+
 template <int DT, int D, int J>
-__global__ __launch_bounds__(256) void gla_scan_kernel(GlaK a) {
-    const int bh = blockIdx.x;
-    const int idx = blockIdx.y * 256 + threadIdx.x;
-    if (idx >= D * J / 4) return;
-    const int dv = idx / (J / 4), j4 = (idx % (J / 4)) * 4;
+__global__ __launch_bounds__(kScanRows * J / 4) void gla_scan_kernel(GlaK a) {
+    constexpr int P = kScanRows + 4;  // LDS row pitch: 8-byte aligned rows, spread banks
+    __shared__ __attribute__((aligned(16))) uint16_t sT[2][2][J * P];
+    const int bh = blockIdx.x, tid = threadIdx.x;
+    const int dvl = tid / (J / 4), j4 = (tid % (J / 4)) * 4;
+    const int dv0 = blockIdx.y * kScanRows, dv = dv0 + dvl;
+    const bool four = a.nplanes == 4;
     f32x4 S = {0.f, 0.f, 0.f, 0.f};
     const int64_t base = (int64_t)bh * a.nc;
     constexpr int PF = 4;  // chunks whose loads are in flight together
@@ -52,8 +61,25 @@ __global__ __launch_bounds__(256) void gla_scan_kernel(GlaK a) {
         }
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
-            if (c0 + u >= a.nc) break;
-            store_state_planes<DT, D, J>(a.s_in + (base + c0 + u) * a.nplanes * D * J, a.nplanes, dv, j4, S);
+            const int c = c0 + u;
+            if (c >= a.nc) break;  // block-uniform
+            uint16_t *dst = a.s_in + (base + c) * a.nplanes * D * J;
+            store_state_planes<DT, D, J>(dst, 2, dv, j4, S);
+            if (four) {
+                uint2 hv, lv;
+                split4(S, hv, lv);
+                uint16_t *th = sT[c & 1][0], *tl = sT[c & 1][1];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t hb = e < 2 ? hv.x : hv.y, lb = e < 2 ? lv.x : lv.y;
+                    th[(j4 + e) * P + dvl] = (uint16_t)((e & 1) ? hb >> 16 : hb & 0xffffu);
+                    tl[(j4 + e) * P + dvl] = (uint16_t)((e & 1) ? lb >> 16 : lb & 0xffffu);
+                }
+                __syncthreads();  // the other buffer was last read before the previous barrier
+                const int j = tid / (kScanRows / 4), c4 = (tid % (kScanRows / 4)) * 4;
+                *(uint2 *)(dst + 2 * D * J + j * D + dv0 + c4) = *(const uint2 *)&th[j * P + c4];
+                *(uint2 *)(dst + 3 * D * J + j * D + dv0 + c4) = *(const uint2 *)&tl[j * P + c4];
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e) S[e] = fmaf(fast_exp2(gl[u][e] * kLog2e), S[e], ds[u][e]);
         }
@@ -286,7 +312,7 @@ template <int DT, int D, int J, bool GEN>
 void launch(const GlaK &k, hipStream_t s) {
     const int nblk = k.B * k.H * k.nc;
     hipLaunchKernelGGL((gla_state_kernel<DT, D, J, GEN, false>), dim3(nblk), dim3(kStateThreads), 0, s, k);
-    hipLaunchKernelGGL((gla_scan_kernel<DT, D, J>), dim3(k.B * k.H, (D * J / 4 + 255) / 256), dim3(256), 0, s, k);
+    hipLaunchKernelGGL((gla_scan_kernel<DT, D, J>), dim3(k.B * k.H, D / kScanRows), dim3(kScanRows * J / 4), 0, s, k);
     hipLaunchKernelGGL((gla_out_kernel<DT, D, J, GEN, false>), dim3(nblk), dim3(NT), 0, s, k);
     hipLaunchKernelGGL((gla_out_kernel<DT, D, J, GEN, true>), dim3(nblk), dim3(NT), 0, s, k);
 }
