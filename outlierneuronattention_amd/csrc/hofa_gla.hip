@@ -38,16 +38,12 @@ constexpr int NT = 128;  // threads of the output kernel
 // directly; planes 2/3 (S, d contiguous), written only for a backward pass,
 // go through a double-buffered LDS transpose so that both layouts leave with
 // contiguous stores.
-constexpr int kScanRows = 16;
-
 template <int DT, int D, int J>
 __global__ __launch_bounds__(kScanRows * J / 4) void gla_scan_kernel(GlaK a) {
-    constexpr int P = kScanRows + 4;  // LDS row pitch: 8-byte aligned rows, spread banks
-    __shared__ __attribute__((aligned(16))) uint16_t sT[2][2][J * P];
+    __shared__ __attribute__((aligned(16))) uint16_t sT[2][2][J * kScanPitch];
     const int bh = blockIdx.x, tid = threadIdx.x;
     const int dvl = tid / (J / 4), j4 = (tid % (J / 4)) * 4;
     const int dv0 = blockIdx.y * kScanRows, dv = dv0 + dvl;
-    const bool four = a.nplanes == 4;
     f32x4 S = {0.f, 0.f, 0.f, 0.f};
     const int64_t base = (int64_t)bh * a.nc;
     constexpr int PF = 4;  // chunks whose loads are in flight together
@@ -63,23 +59,8 @@ __global__ __launch_bounds__(kScanRows * J / 4) void gla_scan_kernel(GlaK a) {
         for (int u = 0; u < PF; ++u) {
             const int c = c0 + u;
             if (c >= a.nc) break;  // block-uniform
-            uint16_t *dst = a.s_in + (base + c) * a.nplanes * D * J;
-            store_state_planes<DT, D, J>(dst, 2, dv, j4, S);
-            if (four) {
-                uint2 hv, lv;
-                split4(S, hv, lv);
-                uint16_t *th = sT[c & 1][0], *tl = sT[c & 1][1];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t hb = e < 2 ? hv.x : hv.y, lb = e < 2 ? lv.x : lv.y;
-                    th[(j4 + e) * P + dvl] = (uint16_t)((e & 1) ? hb >> 16 : hb & 0xffffu);
-                    tl[(j4 + e) * P + dvl] = (uint16_t)((e & 1) ? lb >> 16 : lb & 0xffffu);
-                }
-                __syncthreads();  // the other buffer was last read before the previous barrier
-                const int j = tid / (kScanRows / 4), c4 = (tid % (kScanRows / 4)) * 4;
-                *(uint2 *)(dst + 2 * D * J + j * D + dv0 + c4) = *(const uint2 *)&th[j * P + c4];
-                *(uint2 *)(dst + 3 * D * J + j * D + dv0 + c4) = *(const uint2 *)&tl[j * P + c4];
-            }
+            store_state_tile<DT, D, J>(a.s_in + (base + c) * a.nplanes * D * J, a.nplanes, dv0, dvl, j4, S,
+                                       sT[c & 1][0], sT[c & 1][1]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) S[e] = fmaf(fast_exp2(gl[u][e] * kLog2e), S[e], ds[u][e]);
         }

@@ -192,11 +192,11 @@ __global__ __launch_bounds__(256) void gla_bwd_epilogue_kernel(GlaBwdK a) {
 
 // ---------------------------------------------------------------- 3. reverse scan
 template <int DT, int D, int J>
-__global__ __launch_bounds__(256) void gla_bwd_scan_kernel(GlaBwdK a) {
-    const int bh = blockIdx.x;
-    const int idx = blockIdx.y * 256 + threadIdx.x;
-    if (idx >= D * J / 4) return;
-    const int dv = idx / (J / 4), j4 = (idx % (J / 4)) * 4;
+__global__ __launch_bounds__(kScanRows * J / 4) void gla_bwd_scan_kernel(GlaBwdK a) {
+    __shared__ __attribute__((aligned(16))) uint16_t sT[2][2][J * kScanPitch];
+    const int bh = blockIdx.x, tid = threadIdx.x;
+    const int dvl = tid / (J / 4), j4 = (tid % (J / 4)) * 4;
+    const int dv0 = blockIdx.y * kScanRows, dv = dv0 + dvl;
     const int nc = a.f.nc;
     const int64_t base = (int64_t)bh * nc;
     f32x4 X = {0.f, 0.f, 0.f, 0.f};
@@ -211,8 +211,10 @@ __global__ __launch_bounds__(256) void gla_bwd_scan_kernel(GlaBwdK a) {
         }
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
-            if (c0 - u < 0) break;
-            store_state_planes<DT, D, J>(a.ds_end + (base + c0 - u) * 4 * D * J, 4, dv, j4, X);
+            const int c = c0 - u;
+            if (c < 0) break;  // block-uniform
+            store_state_tile<DT, D, J>(a.ds_end + (base + c) * 4 * D * J, 4, dv0, dvl, j4, X, sT[c & 1][0],
+                                       sT[c & 1][1]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) X[e] = fmaf(fast_exp2(gl[u][e] * kLog2e), X[e], dh[u][e]);
         }
@@ -778,7 +780,7 @@ void launch(const GlaBwdK &k, hipStream_t s) {
     fk.ws_ds = k.ws_dh;
     fk.ws_gl = k.ws_gl;
     hipLaunchKernelGGL((gla_state_kernel<DT, D, J, GEN, true>), dim3(nbh * k.f.nc), dim3(kStateThreads), 0, s, fk);
-    hipLaunchKernelGGL((gla_bwd_scan_kernel<DT, D, J>), dim3(nbh, (D * J / 4 + 255) / 256), dim3(256), 0, s, k);
+    hipLaunchKernelGGL((gla_bwd_scan_kernel<DT, D, J>), dim3(nbh, D / kScanRows), dim3(kScanRows * J / 4), 0, s, k);
     hipLaunchKernelGGL((gla_bwd_chunk_kernel<DT, D, J, GEN, false>), dim3(nbh * k.f.nc), dim3(NTB), 0, s, k);
     hipLaunchKernelGGL((gla_bwd_chunk_kernel<DT, D, J, GEN, true>), dim3(nbh * k.f.nc), dim3(NTB), 0, s, k);
     hipLaunchKernelGGL((gla_bwd_dlg_kernel<D, J, GEN>), dim3(nbh), dim3(256), 0, s, k);

@@ -321,5 +321,35 @@ __device__ __forceinline__ void store_state_planes(uint16_t *dst, int nplanes, i
     }
 }
 
+// The scans run one block per (head, kScanRows value rows) with thread
+// (dvl, j4) carrying S[j4..j4+3][dv0 + dvl]; kScanRows * J / 4 threads.
+constexpr int kScanRows = 16;
+constexpr int kScanPitch = kScanRows + 4;  // LDS row pitch: 8-byte aligned rows, spread banks
+
+// Store one chunk's state from a scan block: planes 0/1 (S^T) directly; with
+// four planes, planes 2/3 (S, d contiguous) through the LDS tile
+// sT[2][J * kScanPitch] (hi, lo), so that they also leave with contiguous
+// stores.  Contains a barrier when nplanes == 4 (block-uniform); callers
+// alternate between two tiles, so one barrier per chunk suffices.
+template <int DT, int D, int J>
+__device__ __forceinline__ void store_state_tile(uint16_t *dst, int nplanes, int dv0, int dvl, int j4,
+                                                 const f32x4 &S, uint16_t *th, uint16_t *tl) {
+    store_state_planes<DT, D, J>(dst, 2, dv0 + dvl, j4, S);
+    if (nplanes != 4) return;
+    uint2 hv, lv;
+    split4(S, hv, lv);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t hb = e < 2 ? hv.x : hv.y, lb = e < 2 ? lv.x : lv.y;
+        th[(j4 + e) * kScanPitch + dvl] = (uint16_t)((e & 1) ? hb >> 16 : hb & 0xffffu);
+        tl[(j4 + e) * kScanPitch + dvl] = (uint16_t)((e & 1) ? lb >> 16 : lb & 0xffffu);
+    }
+    __syncthreads();  // the other tile was last read before the previous barrier
+    const int tid = threadIdx.x;
+    const int j = tid / (kScanRows / 4), c4 = (tid % (kScanRows / 4)) * 4;
+    *(uint2 *)(dst + 2 * D * J + j * D + dv0 + c4) = *(const uint2 *)&th[j * kScanPitch + c4];
+    *(uint2 *)(dst + 3 * D * J + j * D + dv0 + c4) = *(const uint2 *)&tl[j * kScanPitch + c4];
+}
+
 }  // namespace gla
 }  // namespace hofa
