@@ -151,3 +151,104 @@ def test_decode_wrapper_checks_extents_on_host():
     for shape in [(1, H, 1, J + 1), (H, J - 1), (H * J + 1,)]:
         with pytest.raises(_lib.HofaError):
             log_alpha_strides(torch.zeros(shape), H, J)
+
+
+# ---------------------------------------------------------------- single-token block entry points
+def _rows_args(B=2, K=1024, N=512, dt=_lib.HOFA_BF16):
+    a = _lib.RowsLinearArgs()
+    a.B, a.K, a.N, a.dtype = B, K, N, dt
+    a.x, a.x_stride = 4096, K
+    a.w = 8192
+    a.y, a.y_stride = 16384, N
+    return a
+
+
+@pytest.mark.parametrize("field,value,code,text", [
+    ("B", 5, -2, "B=5"),
+    ("B", 0, -2, "B=0"),
+    ("K", 1020, -2, "multiple of 8"),
+    ("K", 8192, -2, "at most 4096"),
+    ("N", 0, -1, "N=0"),
+    ("dtype", _lib.HOFA_F32, -2, "bf16 or f16"),
+    ("act", 2, -1, "act=2"),
+    ("w", None, -1, "NULL"),
+    ("y_stride", 100, -1, "row strides"),
+])
+def test_rows_linear_rejects_bad_arguments(field, value, code, text):
+    lib = _lib.load()
+    a = _rows_args()
+    setattr(a, field, value)
+    rc = lib.hofa_rows_linear(ctypes.byref(a), None)
+    assert rc == code, (rc, lib.hofa_last_error())
+    assert text in lib.hofa_last_error().decode()
+
+
+def test_rows_linear_rejects_misaligned_rows_and_orphan_ln_bias():
+    lib = _lib.load()
+    a = _rows_args()
+    a.w = 8194
+    assert lib.hofa_rows_linear(ctypes.byref(a), None) == -1 and "aligned" in lib.hofa_last_error().decode()
+    a = _rows_args()
+    a.ln_b = 1 << 16
+    assert lib.hofa_rows_linear(ctypes.byref(a), None) == -1 and "ln_b" in lib.hofa_last_error().decode()
+
+
+def _prologue_args(D=64, R=16):
+    a = _lib.DecodePrologueArgs()
+    a.B, a.H, a.D, a.R, a.dtype, a.cache_len = 1, 4, D, R, _lib.HOFA_BF16, 32
+    a.qkv, a.qkv_stride = 4096, 3 * 4 * D
+    a.gate_w = a.gate_b = a.mix_w = a.mix_b = 8192
+    a.pos = a.cache_k = a.cache_v = a.log_gamma = a.mix = 16384
+    return a
+
+
+@pytest.mark.parametrize("field,value,code,text", [
+    ("D", 96, -2, "D=96"),
+    ("R", 15, -2, "R=15"),
+    ("R", 64, -2, "R=64"),
+    ("dtype", _lib.HOFA_F32, -2, "bf16 or f16"),
+    ("qkv_stride", 10, -1, "qkv_stride"),
+    ("pos", None, -1, "NULL"),
+])
+def test_decode_prologue_rejects_bad_arguments(field, value, code, text):
+    lib = _lib.load()
+    a = _prologue_args()
+    setattr(a, field, value)
+    rc = lib.hofa_decode_prologue(ctypes.byref(a), None)
+    assert rc == code, (rc, lib.hofa_last_error())
+    assert text in lib.hofa_last_error().decode()
+
+
+def test_decode_prologue_needs_a_mix_source_and_paired_tables():
+    lib = _lib.load()
+    a = _prologue_args()
+    a.mix_w = a.mix_b = None
+    assert lib.hofa_decode_prologue(ctypes.byref(a), None) == -1 and "fixed_mix" in lib.hofa_last_error().decode()
+    a = _prologue_args()
+    a.cos, a.rope_rows = 1 << 16, 8
+    assert lib.hofa_decode_prologue(ctypes.byref(a), None) == -1 and "cos and sin" in lib.hofa_last_error().decode()
+    a = _prologue_args()
+    a.cos = a.sin = 1 << 16
+    a.rope_rows, a.rope_dtype = 8, _lib.HOFA_F16
+    assert lib.hofa_decode_prologue(ctypes.byref(a), None) == -1 and "rope_dtype" in lib.hofa_last_error().decode()
+
+
+def test_decode_advance_rejects_bad_arguments():
+    lib = _lib.load()
+    a = _lib.DecodeAdvanceArgs()
+    a.B, a.d_model, a.vocab, a.dtype, a.out_cols = 5, 64, 100, _lib.HOFA_BF16, 8
+    a.argmax = a.emb = a.x = a.tok = a.out = a.col = a.pos = a.seq_len = 4096
+    assert lib.hofa_decode_advance(ctypes.byref(a), None) == -2 and "B=5" in lib.hofa_last_error().decode()
+    a.B, a.out_cols = 2, 0
+    assert lib.hofa_decode_advance(ctypes.byref(a), None) == -1 and "out_cols=0" in lib.hofa_last_error().decode()
+    a.out_cols, a.tok = 8, None
+    assert lib.hofa_decode_advance(ctypes.byref(a), None) == -1 and "NULL" in lib.hofa_last_error().decode()
+
+
+def test_decode_layer_wrappers_require_gpu_tensors():
+    from outlierneuronattention_amd.decode_layer import rows_linear
+    w = torch.zeros(8, 16, dtype=torch.bfloat16)
+    with pytest.raises(_lib.HofaError, match="GPU only"):
+        rows_linear(torch.zeros(1, 16, dtype=torch.bfloat16), w, torch.zeros(1, 8, dtype=torch.bfloat16))
+    with pytest.raises(_lib.HofaError, match="bf16/f16"):
+        rows_linear(torch.zeros(1, 16), w.float(), torch.zeros(1, 8))
