@@ -185,3 +185,47 @@ def test_fused_graph_decoder_matches_module_op_decoder(B, alpha):
         for c_f, c_r in zip(fus.caches[i], ref.caches[i]):
             d = (c_f[:, :, :N + steps].float() - c_r[:, :, :N + steps].float()).abs().max().item()
             assert d <= 3e-2 * max(1.0, c_r.float().abs().max().item())
+
+
+@pytest.mark.parametrize("variant", ["per_layer_r_dh128", "fixed_blend_dh128"])
+def test_fused_decoder_variants_match_module_op_decoder(variant):
+    """The reference's 350M-style schedule varies r per layer at d_h = 128
+    (training/training_config.py:407-422: r = [64, 32, 32] + [16]*18 + [32, 32, 64]);
+    a three-layer U-shape r = [64, 16, 32] and the fixed-blend ablation
+    (src/HybridOutlierFactorizedAttention.py:40-41) decode through the fused
+    step exactly as through the module's own ops (tolerances as above)."""
+    from outlierneuronattention_amd.config import ModelConfig
+    from outlierneuronattention_amd.decode_loop import GreedyGraphDecoder
+    from outlierneuronattention_amd.HybridOutlierFactorizedAttention import SubwordLM
+    fixed = variant == "fixed_blend_dh128"
+    r = [32, 32] if fixed else [64, 16, 32]
+    cfg = ModelConfig(d_model=256, num_heads=2, num_layers=len(r), r=r, fixed_blend_weight=fixed, device=DEV)
+    torch.manual_seed(17)
+    m = SubwordLM(512, cfg)
+    with torch.no_grad():
+        for layer in m.layers:
+            at = layer.attn
+            at.gate_proj.weight.normal_(0, 0.3)
+            if fixed:
+                at.fixed_mix.normal_(0, 1.0)
+            else:
+                at.mix_proj.weight.normal_(0, 0.3)
+            at.gla_scale.uniform_(0.5, 1.5)
+        m.lm_head.weight.mul_(8.0)
+    m = m.to(DEV, torch.bfloat16).eval()
+    assert [layer.attn.d_head for layer in m.layers] == [128] * len(r)
+    B, N, steps = 2, 70, 8
+    ids = torch.randint(0, 512, (B, N), generator=torch.Generator().manual_seed(5)).to(DEV)
+    ref = GreedyGraphDecoder(m, B, N + steps + 2, fused=False)
+    fus = GreedyGraphDecoder(m, B, N + steps + 2, fused=True)
+    ref.prefill(ids)
+    fus.prefill(ids)
+    for s in range(steps):
+        tr = ref.decode(1).clone()
+        tf = fus.decode(1).clone()
+        torch.cuda.synchronize()
+        scale = ref.logits.float().abs().max().item()
+        err = (fus.logits.float() - ref.logits.float()).abs().max().item()
+        print(f"{variant} step {s}: tokens {tf.tolist()} vs {tr.tolist()}, logit err {err:.3e} of {scale:.3e}")
+        assert err <= 3e-2 * scale
+        assert torch.equal(tf, tr)
