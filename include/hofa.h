@@ -270,10 +270,11 @@ int hofa_gla_bwd(const hofa_gla_bwd_args_t *args, void *workspace, size_t worksp
  *   t       = round(GELU_erf(t))                       act = 1
  *   t       = round(t * scale)                         n < scale_cols
  *   y[b, n] = round(res[b, n] + t)                     res optional, may alias y
- * With argmax non-NULL it also folds max_n y[b, n] (first index on ties)
- * into argmax[b] as a 64-bit key (order-preserving value bits << 32 |
- * 0xffffffff - n) by atomic max; argmax[] must hold 0 before the call
- * (hofa_decode_advance clears it).  Replaces, for one token, nn.LayerNorm +
+ * With argmax non-NULL it also writes, for every batch row b and every block
+ * i of 16 output rows, the block's greatest key of y[b, n] (order-preserving
+ * value bits << 32 | 0xffffffff - n, so ties go to the first index) to
+ * argmax[b * ceil(N/16) + i]; argmax holds B * ceil(N/16) entries and needs
+ * no initialisation.  Replaces, for one token, nn.LayerNorm +
  * nn.Linear (+ nn.GELU) + the residual add of TransformerBlock.forward_step
  * (src/HybridOutlierFactorizedAttention.py:447-451), the scaled W_q/W_k/W_v
  * projections of forward_step (:223-235), out_proj, and SubwordLM.lm_head
@@ -342,10 +343,11 @@ int hofa_decode_prologue(const hofa_decode_prologue_args_t *args, void *stream);
 
 /*
  * hofa_decode_advance: ends one greedy step.  For each batch row b the token
- * idx = the index in argmax[b] (see hofa_rows_linear) is written to tok[b]
+ * idx = the index in the greatest of argmax[b * ceil(vocab/16) + i] (the LM
+ * head's per-block keys, see hofa_rows_linear) is written to tok[b]
  * and out[b, *col] (when *col < out_cols), and emb[idx, :] (the tied
  * embedding, [vocab, d_model]) becomes x[b, :], the next step's input; then
- * argmax[] is cleared and *col, *pos and *seq_len advance by one.  Replaces
+ * *col, *pos and *seq_len advance by one.  Replaces
  * the greedy feedback of the generation loop (src/inference.py:220-239).
  * Supported: 1 <= B <= 4; emb and x share dtype (bf16 | f16).
  * ---------------------------------------------------------------------- */
@@ -353,7 +355,7 @@ typedef struct {
     int32_t B, d_model, vocab, dtype;
     int32_t out_cols;
     int32_t reserved;
-    unsigned long long *argmax;
+    const unsigned long long *argmax;
     const void *emb;
     void *x;
     int64_t x_stride;

@@ -14,17 +14,17 @@
 //       rows and streams their weights with 16-byte loads, lane l taking
 //       8-element pieces l, l+64, ...  The epilogue rounds like the module's
 //       chain of 16-bit ops: +bias, GELU (erf), *scale on leading columns,
-//       +residual, each rounded to the storage type.  With argmax it also
-//       folds a (value, -index) key per batch row into a 64-bit atomic max.
+//       +residual, each rounded to the storage type.  With argmax every block
+//       also writes its best (value, -index) key per batch row to its own slot.
 //   decode_prologue_kernel   one wave per (b, h): gate and mix logits on the
 //       pre-RoPE scaled Q/K (:67-95), log_gamma = logsigmoid(-gate), mix =
 //       sigmoid, RoPE of the outlier channels at the device position (:365-375),
 //       and the cache append at that row (:382-387); rotated q/k are written
 //       back in place so the decode kernel reads them from the projection.
 //   decode_advance_kernel    one block: the greedy token of every batch row
-//       from the argmax keys, its embedding row as the next input, the output
-//       column, and the position counters (pos, seq_len, col) advanced; the
-//       keys are cleared for the next step (no memset node in a graph).
+//       (the greatest of the LM head's per-block keys), its embedding row as
+//       the next input, the output column, and the position counters (pos,
+//       seq_len, col) advanced.
 #include "hofa_common.h"
 
 namespace hofa {
@@ -192,11 +192,11 @@ __global__ __launch_bounds__(LT) void rows_linear_kernel(RowsLinK a) {
             if (lane == 0) best[b][w] = k;
         }
         __syncthreads();
-        if (tid < a.B) {
+        if (tid < a.B) {  // one slot per (row, block): no atomics; the feedback kernel reduces the slots
             unsigned long long k = best[tid][0];
 #pragma unroll
             for (int i = 1; i < LW; ++i) k = best[tid][i] > k ? best[tid][i] : k;
-            atomicMax(a.argmax + tid, k);
+            a.argmax[(int64_t)tid * gridDim.x + blockIdx.x] = k;
         }
     }
 }
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(LT) void rows_linear_kernel(RowsLinK a) {
 template <int DT, int NB>
 int launch_rows(const RowsLinK &k, hipStream_t s) {
     const size_t lds = (size_t)NB * k.K * 2;
-    if (k.N >= 16384) {
+    if (k.N >= 16384 || k.argmax) {  // argmax slots assume 16 rows per block
         constexpr int RPW = 4;
         hipLaunchKernelGGL((rows_linear_kernel<DT, NB, RPW>), dim3((k.N + LW * RPW - 1) / (LW * RPW)), dim3(LT), lds,
                            s, k);
@@ -309,22 +309,40 @@ __global__ __launch_bounds__(64) void decode_prologue_kernel(PrologueK a) {
 
 // ------------------------------------------------------------------ advance
 struct AdvanceK {
-    unsigned long long *argmax;
+    const unsigned long long *argmax;  // [B][slots] per-block keys of the LM head
     const void *emb;
     void *x;
     int64_t *tok, *out, *col, *pos;
     int32_t *seq_len;
     int64_t x_st, out_st;
-    int B, Dm, V, out_cols;
+    int B, Dm, V, out_cols, slots;
 };
 
 template <int DT>
 __global__ __launch_bounds__(256) void decode_advance_kernel(AdvanceK a) {
     using st = typename Stor<DT>::type;
-    const int tid = threadIdx.x;
+    __shared__ unsigned long long s_best[4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t col = *a.col;
     for (int b = 0; b < a.B; ++b) {
-        const unsigned long long key = a.argmax[b];
+        // greatest key over the LM head's per-block slots of row b
+        unsigned long long key = 0ull;
+        for (int i = tid; i < a.slots; i += 256) {
+            const unsigned long long k = a.argmax[(int64_t)b * a.slots + i];
+            key = k > key ? k : key;
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const uint32_t lo = __shfl_xor((uint32_t)key, off), hi = __shfl_xor((uint32_t)(key >> 32), off);
+            const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+            key = o > key ? o : key;
+        }
+        if (lane == 0) s_best[w] = key;
+        __syncthreads();
+        key = s_best[0];
+#pragma unroll
+        for (int i = 1; i < 4; ++i) key = s_best[i] > key ? s_best[i] : key;
+        __syncthreads();  // s_best is reused by the next row
         const int64_t idx = min((int64_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull)), (int64_t)a.V - 1);
         const st *er = (const st *)a.emb + idx * a.Dm;
         st *xr = (st *)a.x + b * a.x_st;
@@ -334,8 +352,7 @@ __global__ __launch_bounds__(256) void decode_advance_kernel(AdvanceK a) {
             if (col < a.out_cols) a.out[b * a.out_st + col] = idx;
         }
     }
-    __syncthreads();  // every key and counter read above happens before the writes below
-    if (tid < a.B) a.argmax[tid] = 0ull;
+    __syncthreads();  // every counter read above happens before the writes below
     if (tid == 0) {
         *a.col = col + 1;
         *a.pos = *a.pos + 1;
@@ -426,6 +443,7 @@ extern "C" int hofa_decode_advance(const hofa_decode_advance_args_t *a, void *st
     k.argmax = a->argmax; k.emb = a->emb; k.x = a->x; k.tok = a->tok; k.out = a->out; k.col = a->col;
     k.pos = a->pos; k.seq_len = a->seq_len; k.x_st = a->x_stride; k.out_st = a->out_stride;
     k.B = a->B; k.Dm = a->d_model; k.V = a->vocab; k.out_cols = a->out_cols;
+    k.slots = (a->vocab + 15) / 16;
     hipStream_t s = (hipStream_t)stream;
     if (a->dtype == HOFA_BF16) hipLaunchKernelGGL((decode_advance_kernel<HOFA_BF16>), dim3(1), dim3(256), 0, s, k);
     else hipLaunchKernelGGL((decode_advance_kernel<HOFA_F16>), dim3(1), dim3(256), 0, s, k);

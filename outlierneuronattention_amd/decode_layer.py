@@ -34,13 +34,28 @@ def _rows(t: torch.Tensor, name: str) -> torch.Tensor:
     return t
 
 
+def argmax_slots(n: int) -> int:
+    """Greedy-key slots per batch row of a row-linear over ``n`` outputs (one per 16-row block)."""
+    return (n + 15) // 16
+
+
+def greedy_from_keys(keys: torch.Tensor, B: int, n: int) -> torch.Tensor:
+    """Token index per batch row from the per-block keys (host-side mirror of
+    the feedback kernel's reduction, for tests): keys are unsigned 64-bit
+    ``value bits << 32 | 0xffffffff - index`` stored as int64."""
+    k = keys[:B * argmax_slots(n)].view(B, -1) ^ torch.iinfo(torch.int64).min  # unsigned order as signed
+    best = k.max(dim=1).values ^ torch.iinfo(torch.int64).min
+    return 0xFFFFFFFF - (best & 0xFFFFFFFF)
+
+
 def rows_linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, bias: Optional[torch.Tensor] = None,
                 ln: Optional[tuple] = None, gelu: bool = False, scale: float = 1.0, scale_cols: int = 0,
                 res: Optional[torch.Tensor] = None, argmax: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``out[b] = res[b] + (GELU?)(LN?(x[b]) @ weight.T + bias)`` with ``scale``
     applied to the first ``scale_cols`` outputs; ``ln = (weight, bias, eps)``
-    of an ``nn.LayerNorm``.  ``argmax`` (int64 ``[B]``, zero on entry) also
-    collects each row's greedy token key.  ``res`` may be ``out``."""
+    of an ``nn.LayerNorm``.  ``argmax`` (int64, ``B * argmax_slots(N)``
+    entries) also receives each 16-row block's greedy key per row (see
+    ``greedy_from_keys``).  ``res`` may be ``out``."""
     x2, o2 = _rows(x, "x"), _rows(out, "out")
     B, K = x2.shape
     N = weight.shape[0]
@@ -76,8 +91,9 @@ def rows_linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, bias: 
         a.res, a.res_stride = r2.data_ptr(), r2.stride(0)
     a.y, a.y_stride = o2.data_ptr(), o2.stride(0)
     if argmax is not None:
-        if argmax.dtype != torch.int64 or argmax.numel() < B:
-            raise _lib.HofaError("argmax: expected an int64 tensor of at least B elements")
+        if argmax.dtype != torch.int64 or argmax.numel() < B * argmax_slots(N) or not argmax.is_contiguous():
+            raise _lib.HofaError(f"argmax: expected a contiguous int64 tensor of at least {B * argmax_slots(N)} "
+                                 "elements")
         a.argmax = argmax.data_ptr()
     lib = _lib.load()
     _lib.check(lib.hofa_rows_linear(ctypes.byref(a), _lib.stream_handle(x.device)), "rows_linear")
@@ -129,8 +145,8 @@ def decode_prologue(attn, qkv: torch.Tensor, cache_k: torch.Tensor, cache_v: tor
 
 def decode_advance(argmax: torch.Tensor, emb: torch.Tensor, x: torch.Tensor, tok: torch.Tensor, out: torch.Tensor,
                    col: torch.Tensor, pos: torch.Tensor, seq_len: torch.Tensor) -> None:
-    """End of a greedy step: tokens from the argmax keys into ``tok [B,1]``
-    and ``out[:, col]``, their embedding rows into ``x``, keys cleared,
+    """End of a greedy step: tokens from the LM head's per-block keys into
+    ``tok [B,1]`` and ``out[:, col]``, their embedding rows into ``x``,
     ``col``/``pos``/``seq_len`` advanced by one."""
     x2 = _rows(x, "x")
     B, Dm = x2.shape
@@ -138,8 +154,8 @@ def decode_advance(argmax: torch.Tensor, emb: torch.Tensor, x: torch.Tensor, tok
     if emb.shape != (V, Dm) or not emb.is_contiguous() or emb.dtype != x2.dtype:
         raise _lib.HofaError(f"emb: expected a contiguous [{V}, {Dm}] table of x's dtype")
     if tok.numel() != B or tok.dtype != torch.int64 or out.dtype != torch.int64 or out.shape[0] != B \
-            or out.stride(1) != 1 or argmax.dtype != torch.int64 or argmax.numel() < B:
-        raise _lib.HofaError("decode_advance: tok [B,1], out [B, cols], argmax [B] must be int64")
+            or out.stride(1) != 1 or argmax.dtype != torch.int64 or argmax.numel() < B * argmax_slots(V):
+        raise _lib.HofaError("decode_advance: tok [B,1], out [B, cols], argmax [B * ceil(vocab/16)] must be int64")
     _lib.require_gpu(argmax, emb, x2, tok, out, col, pos, seq_len)
     a = _lib.DecodeAdvanceArgs()
     a.B, a.d_model, a.vocab, a.dtype, a.out_cols = B, Dm, V, _lib.dtype_code(emb), out.shape[1]

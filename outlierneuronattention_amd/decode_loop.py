@@ -44,7 +44,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .decode_layer import decode_advance, decode_prologue, rows_linear
+from .decode_layer import argmax_slots, decode_advance, decode_prologue, rows_linear
 from .HybridOutlierFactorizedAttention import SubwordLM
 from .hofa_decode import decode_args, fused_hofa_decode
 from .modules import apply_rotary_pos_emb
@@ -133,7 +133,8 @@ class GreedyGraphDecoder:
         self.h_mlp = torch.zeros(B, 4 * d, device=dev, dtype=dt)
         self.lg = torch.zeros(B, H, device=dev, dtype=torch.float32)
         self.mix = torch.zeros(B, H, device=dev, dtype=torch.float32)
-        self.keys = torch.zeros(B, dtype=torch.int64, device=dev)  # argmax keys (cleared by the advance kernel)
+        V = m.lm_head.weight.shape[0]
+        self.keys = torch.zeros(B * argmax_slots(V), dtype=torch.int64, device=dev)  # per-block greedy keys
         self.ws = None
 
     # ------------------------------------------------------------------ prefill
@@ -164,7 +165,6 @@ class GreedyGraphDecoder:
         self.logits.copy_(logits)
         if self.fused:
             self.x.copy_(m.token_emb(self.tok)[:, 0])
-            self.keys.zero_()
         self.graphs = None
         return logits
 

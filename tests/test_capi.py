@@ -252,3 +252,28 @@ def test_decode_layer_wrappers_require_gpu_tensors():
         rows_linear(torch.zeros(1, 16, dtype=torch.bfloat16), w, torch.zeros(1, 8, dtype=torch.bfloat16))
     with pytest.raises(_lib.HofaError, match="bf16/f16"):
         rows_linear(torch.zeros(1, 16), w.float(), torch.zeros(1, 8))
+
+
+def test_greedy_key_encoding_orders_values_and_breaks_ties_to_the_first_index():
+    """The LM head's per-block keys: order-preserving float bits << 32 |
+    0xffffffff - index (restated here for float32 values), reduced per row."""
+    import struct
+    from outlierneuronattention_amd.decode_layer import argmax_slots, greedy_from_keys
+
+    def key(v, n):
+        b = struct.unpack("<I", struct.pack("<f", v))[0]
+        k = (~b & 0xFFFFFFFF) if b & 0x80000000 else (b | 0x80000000)
+        u = (k << 32) | (0xFFFFFFFF - n)
+        return u - (1 << 64) if u >= 1 << 63 else u  # stored as int64
+
+    N = 40  # three 16-row blocks per row
+    rows = [[-3.0] * N, [0.5] * N]
+    rows[0][37] = -0.25                    # the maximum among negatives
+    rows[1][5], rows[1][21] = 2.0, 2.0     # a tie across blocks: the first index wins
+    keys = torch.zeros(2 * argmax_slots(N), dtype=torch.int64)
+    for b, vals in enumerate(rows):
+        for blk in range(argmax_slots(N)):
+            best = max(key(vals[n], n) + (1 << 64 if key(vals[n], n) < 0 else 0)
+                       for n in range(16 * blk, min(N, 16 * blk + 16)))
+            keys[b * argmax_slots(N) + blk] = best - (1 << 64) if best >= 1 << 63 else best
+    assert greedy_from_keys(keys, 2, N).tolist() == [37, 5]

@@ -5,7 +5,7 @@
   output, GELU, the ``/ d_h**0.25`` scale, the residual add), to 1e-2
   relative to the largest output (a different fp32 summation order may move
   a value across one bf16 rounding step); the greedy key must name the first
-  maximum of the kernel's own output exactly.
+  maximum of the kernel's own output exactly (first index on ties).
 * ``decode_prologue`` against the module's torch ops for gates, RoPE at the
   device position and the cache append (1e-2 relative: 16-bit logits).
 * the fused greedy decoder against the module-op decoder (``fused=False``)
@@ -51,7 +51,7 @@ def _ref_linear(x, w, bias, ln, gelu, scale, scale_cols, res, dt):
     (4, 256, 20011, True, False, False, False, 0),
 ])
 def test_rows_linear_matches_module_chain(dt, B, K, N, ln, gelu, bias, res, scale_cols):
-    from outlierneuronattention_amd.decode_layer import rows_linear
+    from outlierneuronattention_amd.decode_layer import argmax_slots, greedy_from_keys, rows_linear
     g = torch.Generator().manual_seed(B * 7 + K + N)
     x = (torch.randn(B, K, generator=g) * 2 + 0.5).to(DEV, dt)
     w = (torch.randn(N, K, generator=g) / K ** 0.5).to(DEV, dt)
@@ -62,14 +62,14 @@ def test_rows_linear_matches_module_chain(dt, B, K, N, ln, gelu, bias, res, scal
     scale = 1.0 / 64 ** 0.25
     ref = _ref_linear(x, w, bb, lnp, gelu, scale, scale_cols, rr, dt)
     out = torch.empty(B, N, device=DEV, dtype=dt)
-    keys = torch.zeros(B, dtype=torch.int64, device=DEV)
+    keys = torch.full((B * argmax_slots(N),), -1, dtype=torch.int64, device=DEV)  # every slot gets written
     print(f"rows_linear dt={dt} B={B} K={K} N={N}", flush=True)
     rows_linear(x, w, out, bias=bb, ln=lnp, gelu=gelu, scale=scale, scale_cols=scale_cols,
                 res=None if rr is None else rr.clone(), argmax=keys)
     torch.cuda.synchronize()
     err = (out.float() - ref).abs().max().item()
     assert err <= 1e-2 * ref.abs().max().item(), err
-    idx = 0xFFFFFFFF - (keys & 0xFFFFFFFF)
+    idx = greedy_from_keys(keys, B, N)
     assert torch.equal(idx, out.float().argmax(-1)), (idx, out.float().argmax(-1))
 
 
