@@ -63,13 +63,16 @@ def rows_linear(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, bias: 
         raise _lib.HofaError(f"weight: expected a contiguous [{N}, {K}] matrix, got {tuple(weight.shape)}")
     if o2.shape != (B, N):
         raise _lib.HofaError(f"out: expected [{B}, {N}], got {tuple(o2.shape)}")
+    lw, lb = (None, None) if ln is None else (ln[0], ln[1])
     for t, name in ((x2, "x"), (weight, "weight"), (o2, "out"), (bias, "bias"), (res, "res"),
-                    (None if ln is None else ln[0], "ln.weight")):
+                    (lw, "ln.weight"), (lb, "ln.bias")):
         if t is not None and t.dtype != weight.dtype:
             raise _lib.HofaError(f"{name}: dtype {t.dtype} differs from the weight's {weight.dtype}")
+        if t is not None and t is not x2 and t is not o2 and t is not res and not t.is_contiguous():
+            raise _lib.HofaError(f"{name}: must be contiguous")
     if weight.dtype not in _SIXTEEN_BIT:
         raise _lib.HofaError(f"rows_linear runs on bf16/f16 weights, got {weight.dtype}")
-    _lib.require_gpu(x2, weight, o2, bias, res, argmax)
+    _lib.require_gpu(x2, weight, o2, bias, res, argmax, lw, lb)
     a = _lib.RowsLinearArgs()
     a.B, a.K, a.N, a.dtype = B, K, N, _lib.dtype_code(weight)
     a.act, a.scale_cols, a.scale = int(gelu), int(scale_cols), float(scale)
@@ -118,7 +121,19 @@ def decode_prologue(attn, qkv: torch.Tensor, cache_k: torch.Tensor, cache_v: tor
         raise _lib.HofaError("decode_prologue: caches must be contiguous and qkv rows unit-stride")
     if log_gamma.dtype != torch.float32 or mix.dtype != torch.float32 or pos.dtype != torch.int64:
         raise _lib.HofaError("decode_prologue: log_gamma/mix are float32, pos is int64")
-    _lib.require_gpu(qkv, cache_k, cache_v, pos, log_gamma, mix)
+    params = [(attn.gate_proj.weight, (H, 2 * D), "gate_proj.weight"), (attn.gate_proj.bias, (H,), "gate_proj.bias")]
+    if hasattr(attn, "mix_proj"):
+        params += [(attn.mix_proj.weight, (H, 2 * D), "mix_proj.weight"), (attn.mix_proj.bias, (H,), "mix_proj.bias")]
+    elif hasattr(attn, "fixed_mix"):
+        params += [(attn.fixed_mix, (1, H, 1, 1), "fixed_mix")]
+    else:
+        raise _lib.HofaError("decode_prologue: the module has neither mix_proj nor fixed_mix")
+    for t, shape, name in params:
+        if tuple(t.shape) != shape or t.dtype != qkv.dtype or not t.is_contiguous():
+            raise _lib.HofaError(f"decode_prologue: {name} must be a contiguous {shape} tensor of {qkv.dtype}, "
+                                 f"got {tuple(t.shape)} {t.dtype}")
+    rope = (attn.rotary_emb.cos_cached, attn.rotary_emb.sin_cached) if hasattr(attn, "rotary_emb") else (None, None)
+    _lib.require_gpu(qkv, cache_k, cache_v, pos, log_gamma, mix, *(t for t, _, _ in params), *rope)
     a = _lib.DecodePrologueArgs()
     a.B, a.H, a.D, a.R = B, H, D, R
     a.dtype, a.cache_len = _lib.dtype_code(qkv), L

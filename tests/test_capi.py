@@ -277,3 +277,23 @@ def test_greedy_key_encoding_orders_values_and_breaks_ties_to_the_first_index():
                        for n in range(16 * blk, min(N, 16 * blk + 16)))
             keys[b * argmax_slots(N) + blk] = best - (1 << 64) if best >= 1 << 63 else best
     assert greedy_from_keys(keys, 2, N).tolist() == [37, 5]
+
+
+def test_decode_prologue_wrapper_checks_module_parameters():
+    from outlierneuronattention_amd.config import ModelConfig
+    from outlierneuronattention_amd.decode_layer import decode_prologue, rows_linear
+    from outlierneuronattention_amd.HybridOutlierFactorizedAttention import HybridOutlierFactorizedAttention
+    a = HybridOutlierFactorizedAttention(ModelConfig(d_model=128, num_heads=2, num_layers=1, r=16, device="cpu"))
+    B, H, D = 1, 2, 64
+    qkv = torch.zeros(B, 3 * H * D, dtype=torch.bfloat16)
+    ck, cv = torch.zeros(B, H, 8, 16, dtype=torch.bfloat16), torch.zeros(B, H, 8, D, dtype=torch.bfloat16)
+    pos, lg, mix = torch.zeros(1, dtype=torch.int64), torch.zeros(B, H), torch.zeros(B, H)
+    with pytest.raises(_lib.HofaError, match="gate_proj.weight"):  # float32 module, bf16 activations
+        decode_prologue(a, qkv, ck, cv, pos, lg, mix)
+    a = a.to(torch.bfloat16)
+    with pytest.raises(_lib.HofaError, match="GPU only"):
+        decode_prologue(a, qkv, ck, cv, pos, lg, mix)
+    w = torch.zeros(8, 16, dtype=torch.bfloat16)
+    with pytest.raises(_lib.HofaError, match="ln.weight"):
+        rows_linear(torch.zeros(1, 16, dtype=torch.bfloat16), w, torch.zeros(1, 8, dtype=torch.bfloat16),
+                    ln=(torch.ones(16), None, 1e-5))
