@@ -168,9 +168,12 @@ def decode_advance(argmax: torch.Tensor, emb: torch.Tensor, x: torch.Tensor, tok
     V = emb.shape[0]
     if emb.shape != (V, Dm) or not emb.is_contiguous() or emb.dtype != x2.dtype:
         raise _lib.HofaError(f"emb: expected a contiguous [{V}, {Dm}] table of x's dtype")
-    if tok.numel() != B or tok.dtype != torch.int64 or out.dtype != torch.int64 or out.shape[0] != B \
+    if tok.numel() != B or not tok.is_contiguous() or tok.dtype != torch.int64 or out.dtype != torch.int64 \
+            or out.shape[0] != B or any(t.numel() != 1 for t in (col, pos, seq_len)) \
+            or col.dtype != torch.int64 or pos.dtype != torch.int64 or seq_len.dtype != torch.int32 \
             or out.stride(1) != 1 or argmax.dtype != torch.int64 or argmax.numel() < B * argmax_slots(V):
-        raise _lib.HofaError("decode_advance: tok [B,1], out [B, cols], argmax [B * ceil(vocab/16)] must be int64")
+        raise _lib.HofaError("decode_advance: tok [B,1], out [B, cols], argmax [B * ceil(vocab/16)], col and pos "
+                             "(one element) must be int64, seq_len a one-element int32")
     _lib.require_gpu(argmax, emb, x2, tok, out, col, pos, seq_len)
     a = _lib.DecodeAdvanceArgs()
     a.B, a.d_model, a.vocab, a.dtype, a.out_cols = B, Dm, V, _lib.dtype_code(emb), out.shape[1]
