@@ -342,6 +342,24 @@ typedef struct {
 int hofa_decode_prologue(const hofa_decode_prologue_args_t *args, void *stream);
 
 /*
+ * hofa_decode_fused: hofa_decode with hofa_decode_prologue folded into its
+ * launch, for a caller (the greedy graph decoder) that would run the two back
+ * to back.  q, k, v are the pre-RoPE scaled projections (as handed to
+ * hofa_decode_prologue); the position is pos = seq_len - 1 (seq_len_dev or
+ * seq_len); the log_gamma and mix views are not read (they come from the
+ * gates).  The state block of each head computes the gates, rotates the
+ * outlier channels, appends cache row pos, adds the token's own softmax term
+ * as one more split partial and updates the GLA state; the stream blocks
+ * rotate q themselves and read rows [0, pos).  Same results as the two calls
+ * (up to the summation order of the token's score).  Supported: bf16 | f16;
+ * the prologue's B, H, D, R and dtype must match.  Replaces, per token, the
+ * same reference code as the two calls it fuses.
+ * ---------------------------------------------------------------------- */
+size_t hofa_decode_fused_workspace_bytes(const hofa_decode_args_t *args);
+int hofa_decode_fused(const hofa_decode_args_t *args, const hofa_decode_prologue_args_t *prologue,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * hofa_decode_advance: ends one greedy step.  For each batch row b the token
  * idx = the index in the greatest of argmax[b * ceil(vocab/16) + i] (the LM
  * head's per-block keys, see hofa_rows_linear) is written to tok[b]

@@ -137,6 +137,9 @@ EXPORTS = [
     ("hofa_rows_linear", ctypes.c_int, [ctypes.POINTER(RowsLinearArgs), ctypes.c_void_p]),
     ("hofa_decode_prologue", ctypes.c_int, [ctypes.POINTER(DecodePrologueArgs), ctypes.c_void_p]),
     ("hofa_decode_advance", ctypes.c_int, [ctypes.POINTER(DecodeAdvanceArgs), ctypes.c_void_p]),
+    ("hofa_decode_fused_workspace_bytes", ctypes.c_size_t, [ctypes.POINTER(DecodeArgs)]),
+    ("hofa_decode_fused", ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(DecodePrologueArgs),
+                                         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     ("hofa_last_error", ctypes.c_char_p, []),
     ("hofa_version", ctypes.c_int, []),
 ]

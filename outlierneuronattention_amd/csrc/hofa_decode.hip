@@ -56,6 +56,10 @@ struct DecodeKArgs {
     int n_split, tps;
     float qscale;  // sm_scale * log2(e): scores live in the base-2 domain
     float eps;
+    int nslot;     // partials per head: n_split, plus the new token's with the in-kernel prologue
+    // in-kernel prologue (hofa_decode_fused): gates, RoPE and cache append of the new token
+    const void *gate_w, *gate_b, *mix_w, *mix_b, *fixed_mix, *rcos, *rsin;
+    int rope, rope_dt, rope_rows;
 };
 
 template <int DT, int D>
@@ -67,6 +71,22 @@ struct Geometry {
 
 __device__ __forceinline__ int current_len(const DecodeKArgs &a) {
     return a.seq_len_dev ? min(*a.seq_len_dev, a.cache_len) : a.seq_len;
+}
+
+template <int DT>
+__device__ __forceinline__ float rnd_st(float v) {
+    return to_f32<DT>(from_f32<DT>(v));
+}
+
+// One rotated element x' = x cos + rotate_half(x) sin (partner = the element
+// half a rotation away, lower = the element sits in the first half).  16-bit
+// tables round each product as a 16-bit module computes it; f32 tables round
+// once.  The same expression as hofa_decode_prologue, so both paths agree.
+template <int DT>
+__device__ __forceinline__ float rope1(float x, float partner, bool lower, float c, float s, int rope_dt) {
+    const float sg = lower ? -1.f : 1.f;
+    if (rope_dt == HOFA_F32) return rnd_st<DT>(x * c + sg * partner * s);
+    return rnd_st<DT>(rnd_st<DT>(x * c) + rnd_st<DT>(sg * partner * s));
 }
 
 // GLA state update of one head; (1 - mix) * RMSNorm(y_I) * norm_w and mix go to the workspace.
@@ -139,7 +159,132 @@ __device__ void state_block(const DecodeKArgs &a, int bh) {
     if (tid == 0) z[D] = mix;
 }
 
+// The state block with the prologue of the new token folded in: gates from the
+// pre-RoPE q/k, RoPE of the outlier channels at pos = seq_len - 1, the cache
+// append of that row, the token's own softmax partial (m = q.k * scale, l = 1,
+// acc = v) as partial n_split, then the GLA update and inlier epilogue.
 template <int DT, int D, int R>
+__device__ void state_block_pro(const DecodeKArgs &a, int bh) {
+    using st = typename Stor<DT>::type;
+    constexpr int J = D - R;
+    constexpr int DV4 = D / 4;
+    constexpr int RG = kThreads / DV4;  // state rows per pass
+    constexpr int NPASS = (J + RG - 1) / RG;
+    static_assert(R <= 64, "the token's outlier score is one wave's sum");
+    __shared__ float s_q[D], s_k[D], s_v[D], s_g[J];
+    __shared__ float s_red[RG * D];
+    __shared__ float s_gate[2];  // log_gamma, mix
+    const int b = bh / a.H, h = bh % a.H;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int d4 = (tid % DV4) * 4, jr = tid / DV4;
+    const int pos = max(current_len(a) - 1, 0);
+    const float *sin = a.state_in + b * a.st_sb + h * a.st_sh;
+    f32x4 srow[NPASS];
+#pragma unroll
+    for (int i = 0; i < NPASS; ++i) {
+        const int j = jr + i * RG;
+        srow[i] = j < J ? *(const f32x4 *)(sin + j * D + d4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const st *qp = (const st *)a.q + b * a.q_sb + h * a.q_sh;
+    const st *kp = (const st *)a.k + b * a.k_sb + h * a.k_sh;
+    const st *vp = (const st *)a.v + b * a.v_sb + h * a.v_sh;
+    for (int i = tid; i < D; i += kThreads) {
+        s_q[i] = to_f32<DT>(qp[i * a.q_sd]);
+        s_k[i] = to_f32<DT>(kp[i * a.k_sd]);
+        s_v[i] = to_f32<DT>(vp[i * a.v_sd]);
+    }
+    __syncthreads();
+    if (tid < 64) {  // gate and mix logits on the pre-RoPE q, k, rounded as the module's 16-bit einsums
+        const st *gw = (const st *)a.gate_w + h * 2 * D;
+        const st *mw = a.mix_w ? (const st *)a.mix_w + h * 2 * D : nullptr;
+        float g = 0.f, m = 0.f;
+        for (int d = lane; d < D; d += 64) {
+            g = fmaf(s_q[d], to_f32<DT>(gw[d]), fmaf(s_k[d], to_f32<DT>(gw[D + d]), g));
+            if (mw) m = fmaf(s_q[d], to_f32<DT>(mw[d]), fmaf(s_k[d], to_f32<DT>(mw[D + d]), m));
+        }
+        g = wave_sum(g);
+        m = wave_sum(m);
+        if (lane == 0) {
+            const float gl = rnd_st<DT>(g + to_f32<DT>(((const st *)a.gate_b)[h]));
+            const float ng = -gl;
+            s_gate[0] = rnd_st<DT>(fminf(ng, 0.f) - log1pf(expf(-fabsf(ng))));
+            const float ml = mw ? rnd_st<DT>(m + to_f32<DT>(((const st *)a.mix_b)[h]))
+                                : to_f32<DT>(((const st *)a.fixed_mix)[h]);
+            s_gate[1] = rnd_st<DT>(1.f / (1.f + expf(-ml)));
+        }
+    }
+    float qr = 0.f, kr = 0.f;
+    if (a.rope && tid < R) {
+        constexpr int half = R / 2;
+        const int pd = tid < half ? tid + half : tid - half;
+        const int64_t prow = (int64_t)min(pos, a.rope_rows - 1) * R;
+        const float c = load_any(a.rcos, a.rope_dt, prow + tid), sn = load_any(a.rsin, a.rope_dt, prow + tid);
+        qr = rope1<DT>(s_q[tid], s_q[pd], tid < half, c, sn, a.rope_dt);
+        kr = rope1<DT>(s_k[tid], s_k[pd], tid < half, c, sn, a.rope_dt);
+    }
+    __syncthreads();  // the gates and partners above read the unrotated values
+    if (a.rope && tid < R) {
+        s_q[tid] = qr;
+        s_k[tid] = kr;
+    }
+    __syncthreads();
+    // cache append at row pos (read by later calls only: this call streams rows [0, pos))
+    st *ck = (st *)a.cache_k + b * a.ck_sb + h * a.ck_sh + (int64_t)pos * a.ck_sl;
+    st *cv = (st *)a.cache_v + b * a.cv_sb + h * a.cv_sh + (int64_t)pos * a.cv_sl;
+    for (int i = tid; i < R; i += kThreads) ck[i] = from_f32<DT>(s_k[i]);
+    for (int i = tid; i < D; i += kThreads) cv[i] = from_f32<DT>(s_v[i]);
+    // the new token's partial
+    float *pacc = a.ws_acc + ((int64_t)bh * a.nslot + a.n_split) * D;
+    for (int i = tid; i < D; i += kThreads) pacc[i] = s_v[i];
+    if (tid < 64) {
+        const float dot = wave_sum(lane < R ? s_q[lane] * s_k[lane] : 0.f);
+        if (lane == 0) *(float2 *)(a.ws_ml + ((int64_t)bh * a.nslot + a.n_split) * 2) = make_float2(dot * a.qscale, 1.f);
+    }
+    // GLA update on the inlier channels (not rotated) with the token's decay
+    const float lg = s_gate[0];
+    for (int i = tid; i < J; i += kThreads) {
+        float e = lg;
+        if (a.log_alpha) e = lg * expf(load_any(a.log_alpha, a.la_dt, h * a.la_sh + i * a.la_sj));
+        s_g[i] = expf(e);
+    }
+    __syncthreads();
+    float *sout = a.state_out + b * a.so_sb + h * a.so_sh;
+    const f32x4 vv = {s_v[d4], s_v[d4 + 1], s_v[d4 + 2], s_v[d4 + 3]};
+    f32x4 yp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NPASS; ++i) {
+        const int j = jr + i * RG;
+        if (j < J) {
+            const f32x4 sn = s_g[j] * srow[i] + s_k[R + j] * vv;
+            *(f32x4 *)(sout + j * D + d4) = sn;
+            yp += s_q[R + j] * sn;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s_red[jr * D + d4 + c] = yp[c];
+    __syncthreads();
+    float y = 0.f;
+    if (tid < D) {
+#pragma unroll
+        for (int r = 0; r < RG; ++r) y += s_red[r * D + tid];
+    }
+    float ss = wave_sum(y * y);  // D <= 128: waves 0 and 1 hold y
+    __shared__ float s_ss[kWaves];
+    if (lane == 0) s_ss[tid >> 6] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) ss += s_ss[w];
+    const float mix = s_gate[1];
+    float *z = a.ws_z + bh * (D + 4);
+    if (tid < D) {
+        const float nw = load_any(a.norm_w, a.nw_dt, h * a.nw_sh + tid * a.nw_sd);
+        z[tid] = (1.f - mix) * (y * rsqrtf(ss / (float)D + a.eps) * nw);
+    }
+    if (tid == 0) z[D] = mix;
+}
+
+template <int DT, int D, int R, bool PRO>
 __global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeKArgs a) {
     using st = typename Stor<DT>::type;
     using G = Geometry<DT, D>;
@@ -153,7 +298,8 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeKArgs a) 
 
     const int nbh = a.B * a.H;
     if ((int)blockIdx.x < nbh) {
-        state_block<DT, D, R>(a, blockIdx.x);
+        if constexpr (PRO) state_block_pro<DT, D, R>(a, blockIdx.x);
+        else state_block<DT, D, R>(a, blockIdx.x);
         return;
     }
     const int bh = (blockIdx.x - nbh) / a.n_split, split = (blockIdx.x - nbh) % a.n_split;
@@ -164,12 +310,30 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeKArgs a) 
     const int pk = lane % KL, pv = lane % LPR;
     const int tpw = a.tps / kWaves;
     const int ws = split * a.tps + wave * tpw;
-    const int we = min(ws + tpw, seq_len);
+    // with the prologue the newest row is the state block's partial
+    const int we = min(ws + tpw, PRO ? max(seq_len - 1, 0) : seq_len);
 
     const st *qp = (const st *)a.q + b * a.q_sb + h * a.q_sh;
     float qv[EPV];
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) qv[e] = to_f32<DT>(qp[(pk * EPV + e) * a.q_sd]) * a.qscale;
+    for (int e = 0; e < EPV; ++e) qv[e] = to_f32<DT>(qp[(pk * EPV + e) * a.q_sd]);
+    if constexpr (PRO) {  // rotate this lane's q elements; the partner half sits KL/2 lanes away
+        static_assert(KL >= 2, "RoPE partner lanes");
+        if (a.rope) {
+            const int64_t prow = (int64_t)min(max(seq_len - 1, 0), a.rope_rows - 1) * R;
+            float pq[EPV];
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) pq[e] = __shfl_xor(qv[e], KL / 2);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) {
+                const int d = pk * EPV + e;
+                qv[e] = rope1<DT>(qv[e], pq[e], pk < KL / 2, load_any(a.rcos, a.rope_dt, prow + d),
+                                  load_any(a.rsin, a.rope_dt, prow + d), a.rope_dt);
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) qv[e] *= a.qscale;
 
     const st *ckh = (const st *)a.cache_k + b * a.ck_sb + h * a.ck_sh;
     const st *cvh = (const st *)a.cache_v + b * a.cv_sb + h * a.cv_sh;
@@ -274,14 +438,14 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeKArgs a) 
         wgt[w] = s_ml[w][0] == -INFINITY ? 0.f : fast_exp2(s_ml[w][0] - M);
         L += wgt[w] * s_ml[w][1];
     }
-    float *pacc = a.ws_acc + ((int64_t)bh * a.n_split + split) * D;
+    float *pacc = a.ws_acc + ((int64_t)bh * a.nslot + split) * D;
     for (int d = threadIdx.x; d < D; d += kThreads) {
         float o = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) o += wgt[w] * s_acc[w][d];
         pacc[d] = o;
     }
-    if (threadIdx.x == 0) *(float2 *)(a.ws_ml + ((int64_t)bh * a.n_split + split) * 2) = make_float2(M, L);
+    if (threadIdx.x == 0) *(float2 *)(a.ws_ml + ((int64_t)bh * a.nslot + split) * 2) = make_float2(M, L);
 }
 
 // One wave per head.  Every global load is issued before any of them is
@@ -294,7 +458,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeKArgs a) {
     constexpr int DPL = D / 64;  // dims per lane
     const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
     const int lane = threadIdx.x;
-    const int ns = a.n_split;
+    const int ns = a.nslot;
     const float *pacc = a.ws_acc + (int64_t)bh * ns * D;
     const float2 ml = lane < ns ? ((const float2 *)a.ws_ml)[(int64_t)bh * ns + lane] : make_float2(-INFINITY, 0.f);
     float av[NS][DPL];
@@ -409,23 +573,23 @@ size_t ws_bytes(const hofa_decode_args_t *a, int n_split) {
     return acc_bytes(a, n_split) + ml_bytes(a, n_split) + (size_t)a->B * a->H * (a->D + 4) * 4;
 }
 
-template <int DT, int D, int R>
+template <int DT, int D, int R, bool PRO>
 void launch(const DecodeKArgs &k, hipStream_t s) {
     const int bh = k.B * k.H;
-    hipLaunchKernelGGL((decode_stream_kernel<DT, D, R>), dim3(bh + bh * k.n_split), dim3(kThreads), 0, s, k);
-    if (k.n_split <= 8) hipLaunchKernelGGL((decode_merge_kernel<DT, D, 8>), dim3(bh), dim3(64), 0, s, k);
-    else if (k.n_split <= 16) hipLaunchKernelGGL((decode_merge_kernel<DT, D, 16>), dim3(bh), dim3(64), 0, s, k);
-    else if (k.n_split <= 32) hipLaunchKernelGGL((decode_merge_kernel<DT, D, 32>), dim3(bh), dim3(64), 0, s, k);
+    hipLaunchKernelGGL((decode_stream_kernel<DT, D, R, PRO>), dim3(bh + bh * k.n_split), dim3(kThreads), 0, s, k);
+    if (k.nslot <= 8) hipLaunchKernelGGL((decode_merge_kernel<DT, D, 8>), dim3(bh), dim3(64), 0, s, k);
+    else if (k.nslot <= 16) hipLaunchKernelGGL((decode_merge_kernel<DT, D, 16>), dim3(bh), dim3(64), 0, s, k);
+    else if (k.nslot <= 32) hipLaunchKernelGGL((decode_merge_kernel<DT, D, 32>), dim3(bh), dim3(64), 0, s, k);
     else hipLaunchKernelGGL((decode_merge_kernel<DT, D, 64>), dim3(bh), dim3(64), 0, s, k);
 }
 
-template <int DT>
+template <int DT, bool PRO>
 int dispatch(const DecodeKArgs &k, int D, int R, hipStream_t s) {
-    if (D == 64 && R == 16) launch<DT, 64, 16>(k, s);
-    else if (D == 64 && R == 32) launch<DT, 64, 32>(k, s);
-    else if (D == 128 && R == 16) launch<DT, 128, 16>(k, s);
-    else if (D == 128 && R == 32) launch<DT, 128, 32>(k, s);
-    else if (D == 128 && R == 64) launch<DT, 128, 64>(k, s);
+    if (D == 64 && R == 16) launch<DT, 64, 16, PRO>(k, s);
+    else if (D == 64 && R == 32) launch<DT, 64, 32, PRO>(k, s);
+    else if (D == 128 && R == 16) launch<DT, 128, 16, PRO>(k, s);
+    else if (D == 128 && R == 32) launch<DT, 128, 32, PRO>(k, s);
+    else if (D == 128 && R == 64) launch<DT, 128, 64, PRO>(k, s);
     else return HOFA_EUNSUPPORTED;
     return HOFA_OK;
 }
@@ -452,12 +616,25 @@ extern "C" size_t hofa_decode_workspace_bytes(const hofa_decode_args_t *a) {
     return ws_bytes(a, n);
 }
 
-extern "C" int hofa_decode(const hofa_decode_args_t *a, void *workspace, size_t workspace_bytes, void *stream) {
+extern "C" size_t hofa_decode_fused_workspace_bytes(const hofa_decode_args_t *a) {
+    if (validate(a)) return 0;
+    int n, t;
+    plan(a, &n, &t);
+    return ws_bytes(a, n + 1);  // plus the new token's partial per head
+}
+
+namespace {
+
+int run_decode(const hofa_decode_args_t *a, const hofa_decode_prologue_args_t *p, void *workspace,
+               size_t workspace_bytes, void *stream) {
     int rc = validate(a);
     if (rc) return rc;
     int n, t;
     plan(a, &n, &t);
-    const size_t need = ws_bytes(a, n);
+    const int nslot = p ? n + 1 : n;
+    HOFA_REQUIRE(nslot <= kMaxSplit, HOFA_EINVAL, "hofa_decode_fused: %d splits plus the new token exceed %d", n,
+                 kMaxSplit);
+    const size_t need = ws_bytes(a, nslot);
     HOFA_REQUIRE(workspace && workspace_bytes >= need, HOFA_EWORKSPACE,
                  "hofa_decode: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
     HOFA_REQUIRE(((uintptr_t)workspace % 16) == 0, HOFA_EWORKSPACE, "hofa_decode: workspace must be 16-byte aligned");
@@ -472,8 +649,8 @@ extern "C" int hofa_decode(const hofa_decode_args_t *a, void *workspace, size_t 
     k.y = (void *)a->y.data;
     k.seq_len_dev = a->seq_len_dev;
     k.ws_acc = (float *)workspace;
-    k.ws_ml = (float *)((char *)workspace + acc_bytes(a, n));
-    k.ws_z = (float *)((char *)workspace + acc_bytes(a, n) + ml_bytes(a, n));
+    k.ws_ml = (float *)((char *)workspace + acc_bytes(a, nslot));
+    k.ws_z = (float *)((char *)workspace + acc_bytes(a, nslot) + ml_bytes(a, nslot));
     k.q_sb = a->q.stride[0]; k.q_sh = a->q.stride[1]; k.q_sd = a->q.stride[3];
     k.k_sb = a->k.stride[0]; k.k_sh = a->k.stride[1]; k.k_sd = a->k.stride[3];
     k.v_sb = a->v.stride[0]; k.v_sh = a->v.stride[1]; k.v_sd = a->v.stride[3];
@@ -488,19 +665,50 @@ extern "C" int hofa_decode(const hofa_decode_args_t *a, void *workspace, size_t 
     k.y_sb = a->y.stride[0]; k.y_sh = a->y.stride[1]; k.y_sd = a->y.stride[3];
     k.B = a->B; k.H = a->H;
     k.seq_len = a->seq_len; k.cache_len = a->seq_len_dev ? a->cache_len : a->seq_len;
-    k.n_split = n; k.tps = t;
+    k.n_split = n; k.tps = t; k.nslot = nslot;
+    if (p) {
+        k.gate_w = p->gate_w; k.gate_b = p->gate_b; k.mix_w = p->mix_w; k.mix_b = p->mix_b;
+        k.fixed_mix = p->fixed_mix; k.rcos = p->cos; k.rsin = p->sin;
+        k.rope = p->cos != nullptr; k.rope_dt = p->rope_dtype; k.rope_rows = p->rope_rows;
+    }
     k.qscale = a->sm_scale * kLog2e;
     k.eps = a->eps;
 
     hipStream_t s = (hipStream_t)stream;
-    switch (a->q.dtype) {
-        case HOFA_F32: rc = dispatch<HOFA_F32>(k, a->D, a->R, s); break;
-        case HOFA_BF16: rc = dispatch<HOFA_BF16>(k, a->D, a->R, s); break;
-        default: rc = dispatch<HOFA_F16>(k, a->D, a->R, s); break;
+    if (p) {
+        rc = a->q.dtype == HOFA_BF16 ? dispatch<HOFA_BF16, true>(k, a->D, a->R, s)
+                                     : dispatch<HOFA_F16, true>(k, a->D, a->R, s);
+    } else {
+        switch (a->q.dtype) {
+            case HOFA_F32: rc = dispatch<HOFA_F32, false>(k, a->D, a->R, s); break;
+            case HOFA_BF16: rc = dispatch<HOFA_BF16, false>(k, a->D, a->R, s); break;
+            default: rc = dispatch<HOFA_F16, false>(k, a->D, a->R, s); break;
+        }
     }
     if (rc) {
         set_error("hofa_decode: no kernel for this (D, R)");
         return rc;
     }
     return check_launch("hofa_decode");
+}
+
+}  // namespace
+
+extern "C" int hofa_decode(const hofa_decode_args_t *a, void *workspace, size_t workspace_bytes, void *stream) {
+    return run_decode(a, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int hofa_decode_fused(const hofa_decode_args_t *a, const hofa_decode_prologue_args_t *p, void *workspace,
+                                 size_t workspace_bytes, void *stream) {
+    HOFA_REQUIRE(a && p, HOFA_EINVAL, "hofa_decode_fused: args is NULL");
+    HOFA_REQUIRE(p->B == a->B && p->H == a->H && p->D == a->D && p->R == a->R && p->dtype == a->q.dtype, HOFA_EINVAL,
+                 "hofa_decode_fused: prologue (B, H, D, R, dtype) must match the decode arguments");
+    HOFA_REQUIRE(a->q.dtype == HOFA_BF16 || a->q.dtype == HOFA_F16, HOFA_EUNSUPPORTED,
+                 "hofa_decode_fused: dtype %d must be bf16 or f16", a->q.dtype);
+    HOFA_REQUIRE(p->gate_w && p->gate_b && ((p->mix_w && p->mix_b) || p->fixed_mix), HOFA_EINVAL,
+                 "hofa_decode_fused: need gate_w, gate_b and mix_w + mix_b or fixed_mix");
+    HOFA_REQUIRE(!p->cos == !p->sin && (!p->cos || (p->rope_rows > 0 && (p->rope_dtype == HOFA_F32 ||
+                                                                         p->rope_dtype == p->dtype))),
+                 HOFA_EINVAL, "hofa_decode_fused: RoPE tables need cos and sin, rope_rows > 0, f32 or the dtype");
+    return run_decode(a, p, workspace, workspace_bytes, stream);
 }

@@ -109,6 +109,15 @@ def decode_prologue(attn, qkv: torch.Tensor, cache_k: torch.Tensor, cache_v: tor
     token for the attention module ``attn`` (hybrid path); ``qkv [B, 3*H*D]``
     holds the scaled Q | K | V and gets the rotated Q/K back in place;
     writes ``log_gamma`` and ``mix`` (float32 ``[B, H]``)."""
+    a = prologue_args(attn, qkv, cache_k, cache_v, pos, log_gamma, mix)
+    lib = _lib.load()
+    _lib.check(lib.hofa_decode_prologue(ctypes.byref(a), _lib.stream_handle(qkv.device)), "decode_prologue")
+
+
+def prologue_args(attn, qkv: torch.Tensor, cache_k: torch.Tensor, cache_v: torch.Tensor, pos: torch.Tensor,
+                  log_gamma: torch.Tensor, mix: torch.Tensor):
+    """A checked ``hofa_decode_prologue_args_t`` (ctypes) for ``decode_prologue``
+    or ``hofa_decode_fused``."""
     B = qkv.shape[0]
     H, D, R = attn.num_heads, attn.d_head, attn.r
     L = cache_k.shape[2]
@@ -154,8 +163,7 @@ def decode_prologue(attn, qkv: torch.Tensor, cache_k: torch.Tensor, cache_v: tor
     a.pos = pos.data_ptr()
     a.cache_k, a.cache_v = cache_k.data_ptr(), cache_v.data_ptr()
     a.log_gamma, a.mix = log_gamma.data_ptr(), mix.data_ptr()
-    lib = _lib.load()
-    _lib.check(lib.hofa_decode_prologue(ctypes.byref(a), _lib.stream_handle(qkv.device)), "decode_prologue")
+    return a
 
 
 def decode_advance(argmax: torch.Tensor, emb: torch.Tensor, x: torch.Tensor, tok: torch.Tensor, out: torch.Tensor,

@@ -44,7 +44,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .decode_layer import argmax_slots, decode_advance, decode_prologue, rows_linear
+from .decode_layer import argmax_slots, decode_advance, decode_prologue, prologue_args, rows_linear
 from .HybridOutlierFactorizedAttention import SubwordLM
 from .hofa_decode import decode_args, fused_hofa_decode
 from .modules import apply_rotary_pos_emb
@@ -83,7 +83,8 @@ class GreedyGraphDecoder:
     states are allocated once, in the dtype of the model's parameters.
     """
 
-    def __init__(self, model: SubwordLM, batch: int, capacity: int, fused: bool | None = None):
+    def __init__(self, model: SubwordLM, batch: int, capacity: int, fused: bool | None = None,
+                 prologue_in_decode: bool = True):
         for layer in model.layers:
             a = layer.attn
             if not (0 < a.r < a.d_head) or a.forced_mha_heads > 0:
@@ -117,6 +118,9 @@ class GreedyGraphDecoder:
         if fused and not can_fuse:
             raise NotImplementedError("the fused decode step needs bf16/f16 weights, batch <= 4 and d_model <= 1024")
         self.fused = can_fuse if fused is None else bool(fused)
+        # fused step: gates/RoPE/cache append inside the decode launch (hofa_decode_fused), or as
+        # a launch of their own before it (hofa_decode_prologue + hofa_decode)
+        self.prologue_in_decode = bool(prologue_in_decode)
         if self.fused:
             self._init_fused(d)
 
@@ -193,7 +197,9 @@ class GreedyGraphDecoder:
 
     def _step_fused(self, parity: int):
         """The fused greedy step: seven launches per layer, then the LM head
-        with argmax and the feedback kernel; allocates nothing."""
+        with argmax and the feedback kernel; allocates nothing.  With
+        prologue_in_decode the gates/RoPE/cache append run inside the decode
+        launch (six launches per layer)."""
         m, B = self.model, self.B
         x = self.x
         for i, layer in enumerate(m.layers):
@@ -203,7 +209,8 @@ class GreedyGraphDecoder:
             rows_linear(x, self.w_qkv[i], self.qkv, ln=(layer.ln_1.weight, layer.ln_1.bias, layer.ln_1.eps),
                         scale=1.0 / D ** 0.25, scale_cols=2 * HD)
             ck, cv = self.caches[i]
-            decode_prologue(a, self.qkv, ck, cv, self.pos, self.lg, self.mix)
+            if not self.prologue_in_decode:
+                decode_prologue(a, self.qkv, ck, cv, self.pos, self.lg, self.mix)
             q = self.qkv[:, :HD].view(B, H, 1, D)
             k = self.qkv[:, HD:2 * HD].view(B, H, 1, D)
             v = self.qkv[:, 2 * HD:].view(B, H, 1, D)
@@ -213,15 +220,22 @@ class GreedyGraphDecoder:
                                         log_alpha=a.log_alpha if a.learnable_alpha else None,
                                         seq_len_dev=self.seq_len, y=self.y_attn)
             lib = _lib.load()
-            nbytes = lib.hofa_decode_workspace_bytes(ctypes.byref(args))
+            pro = prologue_args(a, self.qkv, ck, cv, self.pos, self.lg, self.mix) if self.prologue_in_decode else None
+            nbytes = (lib.hofa_decode_fused_workspace_bytes if pro is not None
+                      else lib.hofa_decode_workspace_bytes)(ctypes.byref(args))
             if nbytes == 0:
                 _lib.check(-1, "decode step")
             if self.ws is None or self.ws.numel() < nbytes:
                 if torch.cuda.is_current_stream_capturing():
                     raise RuntimeError("decode workspace must be sized before graph capture")
                 self.ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
-            _lib.check(lib.hofa_decode(ctypes.byref(args), self.ws.data_ptr(), self.ws.numel(),
-                                       _lib.stream_handle(self.device)), "decode step")
+            stream = _lib.stream_handle(self.device)
+            if pro is not None:
+                rc = lib.hofa_decode_fused(ctypes.byref(args), ctypes.byref(pro), self.ws.data_ptr(), self.ws.numel(),
+                                           stream)
+            else:
+                rc = lib.hofa_decode(ctypes.byref(args), self.ws.data_ptr(), self.ws.numel(), stream)
+            _lib.check(rc, "decode step")
             del keep
             rows_linear(self.y_attn.view(B, HD), a.out_proj.weight, x, res=x)
             fc1, fc2 = layer.mlp[0], layer.mlp[2]

@@ -160,14 +160,14 @@ def _lm(seed, layers=2, alpha=False):
     return m.to(DEV, torch.bfloat16).eval()
 
 
-@pytest.mark.parametrize("B,alpha", [(1, False), (4, True)])
-def test_fused_graph_decoder_matches_module_op_decoder(B, alpha):
+@pytest.mark.parametrize("B,alpha,pro", [(1, False, True), (4, True, True), (2, False, False)])
+def test_fused_graph_decoder_matches_module_op_decoder(B, alpha, pro):
     from outlierneuronattention_amd.decode_loop import GreedyGraphDecoder
     m = _lm(seed=4 + B, alpha=alpha)
     N, steps = 45, 12
     ids = torch.randint(0, 512, (B, N), generator=torch.Generator().manual_seed(B)).to(DEV)
     ref = GreedyGraphDecoder(m, B, N + steps + 2, fused=False)
-    fus = GreedyGraphDecoder(m, B, N + steps + 2, fused=True)
+    fus = GreedyGraphDecoder(m, B, N + steps + 2, fused=True, prologue_in_decode=pro)
     assert fus.fused and not ref.fused
     ref.prefill(ids)
     fus.prefill(ids)
@@ -229,3 +229,60 @@ def test_fused_decoder_variants_match_module_op_decoder(variant):
         print(f"{variant} step {s}: tokens {tf.tolist()} vs {tr.tolist()}, logit err {err:.3e} of {scale:.3e}")
         assert err <= 3e-2 * scale
         assert torch.equal(tf, tr)
+
+
+def test_prologue_in_decode_matches_prologue_launch():
+    """hofa_decode_fused (gates, RoPE and cache append inside the decode
+    launch, the new token as an extra split partial) against
+    hofa_decode_prologue + hofa_decode on the same step: identical caches,
+    GLA state within 1e-6 relative, outputs within 1e-2 of the largest (the
+    token's score is summed in another order), at a length spanning many
+    splits, with the gate's mix projection and with the fixed blend."""
+    import ctypes
+    from outlierneuronattention_amd import _lib
+    from outlierneuronattention_amd.decode_layer import decode_prologue, prologue_args
+    from outlierneuronattention_amd.hofa_decode import decode_args
+    for fixed in (False, True):
+        a = _attn_module(fixed, seed=3)
+        B, H, D, R, L = 2, 4, 64, 16, 3000
+        g = torch.Generator().manual_seed(21)
+        pos = torch.tensor([2047], dtype=torch.int64, device=DEV)
+        seq = torch.tensor([2048], dtype=torch.int32, device=DEV)
+        qkv0 = torch.randn(B, 3 * H * D, generator=g).to(DEV, torch.bfloat16)
+        ck0 = torch.randn(B, H, L, R, generator=g).to(DEV, torch.bfloat16)
+        cv0 = torch.randn(B, H, L, D, generator=g).to(DEV, torch.bfloat16)
+        s_in = (0.1 * torch.randn(B, H, D - R, D, generator=g)).to(DEV)
+        nw = a.gla_scale.view(H, D)
+        outs = []
+        for fused in (False, True):
+            print(f"prologue-in-decode fixed={fixed} fused={fused}", flush=True)
+            qkv, ck, cv = qkv0.clone(), ck0.clone(), cv0.clone()
+            lg, mix = torch.zeros(B, H, device=DEV), torch.zeros(B, H, device=DEV)
+            s_out = torch.empty_like(s_in)
+            y = torch.empty(B, H, 1, D, device=DEV, dtype=torch.bfloat16)
+            q = qkv[:, :H * D].view(B, H, 1, D)
+            k = qkv[:, H * D:2 * H * D].view(B, H, 1, D)
+            v = qkv[:, 2 * H * D:].view(B, H, 1, D)
+            lib = _lib.load()
+            if not fused:
+                decode_prologue(a, qkv, ck, cv, pos, lg, mix)
+            args, _, keep = decode_args(q, k, v, ck, cv, s_in, s_out, lg, mix, nw, R, L, (D / R) ** 0.5,
+                                        seq_len_dev=seq, y=y)
+            stream = _lib.stream_handle(q.device)
+            if fused:
+                pro = prologue_args(a, qkv, ck, cv, pos, lg, mix)
+                n = lib.hofa_decode_fused_workspace_bytes(ctypes.byref(args))
+                ws = torch.empty(n, dtype=torch.uint8, device=DEV)
+                rc = lib.hofa_decode_fused(ctypes.byref(args), ctypes.byref(pro), ws.data_ptr(), n, stream)
+            else:
+                n = lib.hofa_decode_workspace_bytes(ctypes.byref(args))
+                ws = torch.empty(n, dtype=torch.uint8, device=DEV)
+                rc = lib.hofa_decode(ctypes.byref(args), ws.data_ptr(), n, stream)
+            _lib.check(rc, "decode")
+            torch.cuda.synchronize()
+            outs.append((y.float(), s_out, ck, cv))
+        (y0, s0, ck_a, cv_a), (y1, s1, ck_b, cv_b) = outs
+        print(f"fixed={fixed}: y err {(y0 - y1).abs().max().item():.3e}, state err {(s0 - s1).abs().max().item():.3e}")
+        assert torch.equal(ck_a, ck_b) and torch.equal(cv_a, cv_b)
+        assert (s0 - s1).abs().max().item() <= 1e-6 * s0.abs().max().item()
+        assert (y0 - y1).abs().max().item() <= 1e-2 * y0.abs().max().item()
