@@ -297,3 +297,23 @@ def test_decode_prologue_wrapper_checks_module_parameters():
     with pytest.raises(_lib.HofaError, match="ln.weight"):
         rows_linear(torch.zeros(1, 16, dtype=torch.bfloat16), w, torch.zeros(1, 8, dtype=torch.bfloat16),
                     ln=(torch.ones(16), None, 1e-5))
+
+
+def test_decode_fused_rejects_mismatched_prologue():
+    lib = _lib.load()
+    a = _decode_args(B=1, H=4, D=64, R=16)
+    p = _prologue_args(D=64, R=16)
+    p.H = 2
+    assert lib.hofa_decode_fused(ctypes.byref(a), ctypes.byref(p), None, 0, None) == -1
+    assert "must match" in lib.hofa_last_error().decode()
+    p = _prologue_args(D=64, R=16)
+    p.mix_w = p.mix_b = None
+    assert lib.hofa_decode_fused(ctypes.byref(a), ctypes.byref(p), None, 0, None) == -1
+    assert "fixed_mix" in lib.hofa_last_error().decode()
+    a32 = _decode_args(B=1, H=4, D=64, R=16, dt=_lib.HOFA_F32)
+    p32 = _prologue_args(D=64, R=16)
+    p32.dtype = _lib.HOFA_F32
+    assert lib.hofa_decode_fused(ctypes.byref(a32), ctypes.byref(p32), None, 0, None) == -2
+    assert lib.hofa_decode_fused(ctypes.byref(a), None, None, 0, None) == -1
+    n = lib.hofa_decode_fused_workspace_bytes(ctypes.byref(a))
+    assert n > lib.hofa_decode_workspace_bytes(ctypes.byref(a))  # one more partial per head
