@@ -25,7 +25,7 @@
 //       (the greatest of the LM head's per-block keys), its embedding row as
 //       the next input, the output column, and the position counters (pos,
 //       seq_len, col) advanced.
-#include "hofa_common.h"
+#include "hofa_mfma.h"  // pack2: two floats to one dword of 16-bit values (round to nearest even)
 
 namespace hofa {
 namespace {
@@ -61,54 +61,85 @@ __global__ __launch_bounds__(LT) void rows_linear_kernel(RowsLinK a) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int K = a.K, K8 = K / 8;
 
-    // ---- stage x (LayerNorm'd when ln_w is given) in LDS
+    // ---- stage x (LayerNorm'd when ln_w is given) in LDS.  LayerNorm: every
+    // 16-byte piece of the NB rows is loaded once into registers, the sums and
+    // sums of squares of each row go through one block reduction, and the
+    // normalised pieces are written with 16-byte LDS stores.
     if (a.ln_w) {
-        float s1[NB], s2[NB], mean[NB], rstd[NB];
+        constexpr int MAXP = (NB * 4096 / 8 + LT - 1) / LT;  // pieces per thread at K = 4096
+        const int np = NB * K8;
+        u32x4 xp[MAXP];
+        float s1[NB], s2[NB];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) s1[b] = 0.f;
-        for (int k = tid; k < K; k += LT)
+        for (int b = 0; b < NB; ++b) s1[b] = s2[b] = 0.f;
 #pragma unroll
-            for (int b = 0; b < NB; ++b) s1[b] += to_f32<DT>(((const st *)a.x)[b * a.x_st + k]);
+        for (int j = 0; j < MAXP; ++j) {
+            const int c = tid + LT * j;
+            if (c < np) {
+                const int b = c / K8, k8 = c % K8;
+                xp[j] = *(const u32x4 *)((const st *)a.x + b * a.x_st + 8 * k8);
+                float f[8];
+                unpack16<DT>(xp[j], f);
+                float t1 = 0.f, t2 = 0.f;
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const float t = wave_sum(s1[b]);
-            if (lane == 0) red[0][b][w] = t;
-        }
-        __syncthreads();
+                for (int e = 0; e < 8; ++e) {
+                    t1 += f[e];
+                    t2 = fmaf(f[e], f[e], t2);
+                }
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            float t = 0.f;
-#pragma unroll
-            for (int i = 0; i < LW; ++i) t += red[0][b][i];
-            mean[b] = t / (float)K;
-            s2[b] = 0.f;
-        }
-        for (int k = tid; k < K; k += LT)
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const float d = to_f32<DT>(((const st *)a.x)[b * a.x_st + k]) - mean[b];
-                s2[b] = fmaf(d, d, s2[b]);
+                for (int bb = 0; bb < NB; ++bb)
+                    if (bb == b) {
+                        s1[bb] += t1;
+                        s2[bb] += t2;
+                    }
             }
+        }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            const float t = wave_sum(s2[b]);
-            if (lane == 0) red[1][b][w] = t;
+            const float t1 = wave_sum(s1[b]), t2 = wave_sum(s2[b]);
+            if (lane == 0) {
+                red[0][b][w] = t1;
+                red[1][b][w] = t2;
+            }
         }
         __syncthreads();
+        float mean[NB], rstd[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            float t = 0.f;
+            float t1 = 0.f, t2 = 0.f;
 #pragma unroll
-            for (int i = 0; i < LW; ++i) t += red[1][b][i];
-            rstd[b] = rsqrtf(t / (float)K + a.ln_eps);
+            for (int i = 0; i < LW; ++i) {
+                t1 += red[0][b][i];
+                t2 += red[1][b][i];
+            }
+            mean[b] = t1 / (float)K;
+            rstd[b] = rsqrtf(fmaxf(t2 / (float)K - mean[b] * mean[b], 0.f) + a.ln_eps);
         }
-        for (int k = tid; k < K; k += LT) {
-            const float g = to_f32<DT>(((const st *)a.ln_w)[k]);
-            const float bb = a.ln_b ? to_f32<DT>(((const st *)a.ln_b)[k]) : 0.f;
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const float v = to_f32<DT>(((const st *)a.x)[b * a.x_st + k]);
-                xs[b * K + k] = from_f32<DT>(fmaf((v - mean[b]) * rstd[b], g, bb));
+        for (int j = 0; j < MAXP; ++j) {
+            const int c = tid + LT * j;
+            if (c < np) {
+                const int b = c / K8, k8 = c % K8;
+                float mb = mean[0], rb = rstd[0];
+#pragma unroll
+                for (int bb = 1; bb < NB; ++bb)
+                    if (bb == b) {
+                        mb = mean[bb];
+                        rb = rstd[bb];
+                    }
+                float f[8], g[8], o[8];
+                unpack16<DT>(xp[j], f);
+                unpack16<DT>(*(const u32x4 *)((const st *)a.ln_w + 8 * k8), g);
+                if (a.ln_b) {
+                    unpack16<DT>(*(const u32x4 *)((const st *)a.ln_b + 8 * k8), o);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o[e] = 0.f;
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = fmaf((f[e] - mb) * rb, g[e], o[e]);
+                *(u32x4 *)&xs[b * K + 8 * k8] = u32x4{pack2<DT>(o[0], o[1]), pack2<DT>(o[2], o[3]),
+                                                      pack2<DT>(o[4], o[5]), pack2<DT>(o[6], o[7])};
             }
         }
     } else {
@@ -376,8 +407,9 @@ extern "C" int hofa_rows_linear(const hofa_rows_linear_args_t *a, void *stream) 
     HOFA_REQUIRE(a->act == 0 || a->act == 1, HOFA_EINVAL, "hofa_rows_linear: act=%d not in {0, 1}", a->act);
     HOFA_REQUIRE(a->x && a->w && a->y, HOFA_EINVAL, "hofa_rows_linear: NULL x, w or y");
     HOFA_REQUIRE(a->ln_w || !a->ln_b, HOFA_EINVAL, "hofa_rows_linear: ln_b without ln_w");
-    HOFA_REQUIRE(((uintptr_t)a->w % 16) == 0 && (a->ln_w || (((uintptr_t)a->x % 16) == 0 && a->x_stride % 8 == 0)),
-                 HOFA_EINVAL, "hofa_rows_linear: w (and x without LayerNorm) must be 16-byte aligned rows");
+    HOFA_REQUIRE(((uintptr_t)a->w % 16) == 0 && ((uintptr_t)a->x % 16) == 0 && a->x_stride % 8 == 0 &&
+                     ((uintptr_t)a->ln_w % 16) == 0 && ((uintptr_t)a->ln_b % 16) == 0,
+                 HOFA_EINVAL, "hofa_rows_linear: w, x, ln_w and ln_b must be 16-byte aligned rows");
     HOFA_REQUIRE(a->x_stride >= a->K && a->y_stride >= a->N && (!a->res || a->res_stride >= a->N), HOFA_EINVAL,
                  "hofa_rows_linear: row strides smaller than the row length");
     RowsLinK k{};
