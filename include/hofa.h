@@ -155,7 +155,9 @@ int hofa_attn_fwd(const hofa_attn_fwd_args_t *args, void *stream);
  *   g              [B,H,T,J] f32  strides b, h, t, j; optional general decay (wins over log_gamma)
  *   mix            [B,H,T]        strides b, h, t (needed when fuse_norm_gate)
  *   gla_scale      [H,D]          strides h, d (needed when fuse_norm_gate)
- *   state_out      [B,H,J,D] f32  strides b, h, j, d
+ *   state_out      [B,H,J,D] f32  strides b, h, j, d; with state_pad_rows = P > 0
+ *                  rows J .. J+P-1 (same strides, P <= J) are written with zeros:
+ *                  the reference returns the state zero-padded to [B,H,j_pad,d_pad]
  *   chunk_states   optional 16-bit [B*H][ceil(T/64)][4][D*J] receiving the
  *                  state that enters each chunk as bf16 hi/lo operand pairs
  *                  (hi + lo ~ the fp32 state): planes 0/1 transposed [D][J],
@@ -173,7 +175,7 @@ typedef struct {
     int32_t B, H, T, D, R;
     float eps;
     int32_t fuse_norm_gate;
-    int32_t reserved;
+    int32_t state_pad_rows;
     hofa_view_t q, k, v;
     hofa_view_t log_gamma, log_alpha, g;
     hofa_view_t mix, gla_scale;

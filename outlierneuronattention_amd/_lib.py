@@ -54,7 +54,7 @@ class AttnFwdArgs(ctypes.Structure):
 class GlaFwdArgs(ctypes.Structure):
     _fields_ = [("B", ctypes.c_int32), ("H", ctypes.c_int32), ("T", ctypes.c_int32), ("D", ctypes.c_int32),
                 ("R", ctypes.c_int32), ("eps", ctypes.c_float), ("fuse_norm_gate", ctypes.c_int32),
-                ("reserved", ctypes.c_int32),
+                ("state_pad_rows", ctypes.c_int32),
                 ("q", View), ("k", View), ("v", View),
                 ("log_gamma", View), ("log_alpha", View), ("g", View),
                 ("mix", View), ("gla_scale", View),

@@ -98,10 +98,15 @@ def chunk_gla_inlier_fwd(Q, K, V, log_gamma, r, chunk_size, log_alpha=None, mix_
     J = D - int(r)
     Y = out if out is not None else torch.empty(B, H, T, D, dtype=Q.dtype, device=Q.device)
     _lib.expect_shape(Y, (B, H, T, D), "out")
-    states_out = torch.zeros(B, H, _pow2_at_least_16(J), _pow2_at_least_16(D), dtype=torch.float32, device=Q.device)
+    # the kernel writes the state and the zero rows of its padding (D is 64 or 128: no column padding)
+    j_pad, d_pad = _pow2_at_least_16(J), _pow2_at_least_16(D)
+    if d_pad != D:
+        raise _lib.HofaError(f"chunk_gla_inlier_fwd: head dim {D} unsupported")
+    states_out = torch.empty(B, H, j_pad, d_pad, dtype=torch.float32, device=Q.device)
     state_view = states_out[:, :, :J, :D]
     a, keep = gla_fwd_args(Q, K, V, log_gamma, r, log_alpha, mix_g, gla_scale, Y, state_view, g, eps, chunk_states,
                            n_out, rstd)
+    a.state_pad_rows = j_pad - J
     nbytes = lib.hofa_gla_fwd_workspace_bytes(ctypes.byref(a))
     if nbytes == 0:
         _lib.check(-1, "chunk_gla_inlier_fwd")

@@ -69,6 +69,9 @@ __global__ __launch_bounds__(kScanRows * J / 4) void gla_scan_kernel(GlaK a) {
     float *so = a.state_out + b * a.so_sb + h * a.so_sh;
 #pragma unroll
     for (int e = 0; e < 4; ++e) so[(j4 + e) * a.so_sj + dv * a.so_sd] = S[e];
+    if (j4 < a.pad_rows)  // the zero rows of a padded state (pad_rows <= J, a multiple of 4)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) so[(J + j4 + e) * a.so_sj + dv * a.so_sd] = 0.f;
 }
 
 // FB = false handles the chunks whose decay range is within kSafeRange with
@@ -281,6 +284,8 @@ int validate(const hofa_gla_fwd_args_t *a) {
     HOFA_REQUIRE(!a->fuse_norm_gate || (a->mix.data && a->gla_scale.data), HOFA_EINVAL,
                  "hofa_gla_fwd: fuse_norm_gate needs mix and gla_scale");
     HOFA_REQUIRE(a->state_out.dtype == HOFA_F32, HOFA_EINVAL, "hofa_gla_fwd: state_out must be float32");
+    HOFA_REQUIRE(a->state_pad_rows >= 0 && a->state_pad_rows <= a->D - a->R && a->state_pad_rows % 4 == 0, HOFA_EINVAL,
+                 "hofa_gla_fwd: state_pad_rows=%d must be a multiple of 4 in [0, J]", a->state_pad_rows);
     for (const hofa_view_t *v : {&a->q, &a->k, &a->v})
         HOFA_REQUIRE((int64_t)(a->T + 2 * C) * v->stride[2] * es < (1ll << 31), HOFA_EUNSUPPORTED,
                      "hofa_gla_fwd: one head's q/k/v rows must span less than 2 GiB");
@@ -356,6 +361,7 @@ extern "C" int hofa_gla_fwd(const hofa_gla_fwd_args_t *a, void *workspace, size_
     k.gs_sh = a->gla_scale.stride[0]; k.gs_sd = a->gla_scale.stride[1];
     k.so_sb = a->state_out.stride[0]; k.so_sh = a->state_out.stride[1];
     k.so_sj = a->state_out.stride[2]; k.so_sd = a->state_out.stride[3];
+    k.pad_rows = a->state_pad_rows;
     k.lg_dt = a->log_gamma.dtype; k.la_dt = a->log_alpha.dtype; k.mix_dt = a->mix.dtype; k.gs_dt = a->gla_scale.dtype;
     k.B = a->B; k.H = a->H; k.T = a->T; k.R = a->R;
     k.nc = (a->T + C - 1) / C;

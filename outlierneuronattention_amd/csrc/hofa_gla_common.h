@@ -111,6 +111,7 @@ struct GlaK {
     int B, H, T, R, nc;
     int key_col0;       // first column of the key operand of gla_state_kernel
     int nplanes;        // 2: hi/lo of S^T [D][J]; 4: also hi/lo of S [J][D]
+    int pad_rows;       // state_out rows J .. J+pad_rows-1 to write as zeros
     int fuse;
     float eps;
 };
