@@ -244,19 +244,32 @@ class WorkspaceCache:
     """Scratch buffers keyed by (device, stream, purpose).
 
     One buffer per stream keeps concurrently running streams from sharing
-    scratch; a buffer only grows.  Allocate (warm up) before graph capture.
+    scratch.  A buffer only grows, and a superseded buffer is never freed: a
+    HIP graph captured earlier on the stream keeps the old address in its
+    kernel arguments, so freeing it would let the allocator hand that memory
+    to another tensor that the graph's replays then overwrite.  Growth is at
+    least twofold, so the retired buffers together stay below the size of the
+    live one.  Allocate (warm up) before graph capture.
     """
 
     def __init__(self):
         self._bufs: dict = {}
+        self._retired: list = []
 
     def get(self, device: torch.device, stream: int, tag: str, nbytes: int) -> torch.Tensor:
         key = (device.index, stream, tag)
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            size = max(nbytes, 256)
+            if buf is not None:
+                self._retired.append(buf)
+                size = max(size, 2 * buf.numel())
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
             self._bufs[key] = buf
         return buf
+
+    def retired_bytes(self) -> int:
+        return sum(b.numel() for b in self._retired)
 
 
 WORKSPACES = WorkspaceCache()

@@ -15,6 +15,7 @@ from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libhofa.so")
 ARCH = "gfx950"
@@ -60,10 +61,12 @@ def _jobs() -> list[tuple[str, str, list[str]]]:
 
 
 def _stale(src: str, obj: str) -> bool:
-    """True when obj is missing or older than its source or any csrc header."""
+    """True when obj is missing or older than its source, any csrc header or
+    the C-ABI header (include/*.h, which defines the argument structs)."""
     if not os.path.exists(obj):
         return True
-    deps = [src, *glob.glob(os.path.join(CSRC, "*.h")), os.path.abspath(__file__)]
+    deps = [src, *glob.glob(os.path.join(CSRC, "*.h")), *glob.glob(os.path.join(INCLUDE, "*.h")),
+            os.path.abspath(__file__)]
     return os.path.getmtime(obj) < max(os.path.getmtime(d) for d in deps)
 
 

@@ -1,8 +1,8 @@
 """Model configuration: the constructor contract of the attention modules.
 
-Mirrors ``ModelConfig`` / ``InferenceConfig`` (src/config.py:5-41): the same
-field names, defaults and the ``d_head`` property, so configurations written
-for the reference construct these modules unchanged.
+Mirrors ``ModelConfig`` (src/config.py:5-31): the same field names, defaults
+and the ``d_head`` property, so configurations written for the reference
+construct these modules unchanged.
 """
 from __future__ import annotations
 
@@ -39,12 +39,3 @@ class ModelConfig:
     def d_head(self) -> int:
         return self.d_model // self.num_heads
 
-
-@dataclass
-class InferenceConfig:
-    max_new_tokens: int = 100
-    temperature: float = 0.8
-    top_k: int = 50
-    repetition_penalty: float = 1.15
-    stream: bool = True
-    seed: int = 42

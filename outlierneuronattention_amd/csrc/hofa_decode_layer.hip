@@ -69,9 +69,11 @@ __global__ __launch_bounds__(LT) void rows_linear_kernel(RowsLinK a) {
         constexpr int MAXP = (NB * 4096 / 8 + LT - 1) / LT;  // pieces per thread at K = 4096
         const int np = NB * K8;
         u32x4 xp[MAXP];
-        float s1[NB], s2[NB];
+        // Two passes over the register-held pieces: the mean first, then the
+        // sum of squared deviations (no E[x^2] - mean^2 cancellation).
+        float s1[NB];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) s1[b] = s2[b] = 0.f;
+        for (int b = 0; b < NB; ++b) s1[b] = 0.f;
 #pragma unroll
         for (int j = 0; j < MAXP; ++j) {
             const int c = tid + LT * j;
@@ -80,40 +82,60 @@ __global__ __launch_bounds__(LT) void rows_linear_kernel(RowsLinK a) {
                 xp[j] = *(const u32x4 *)((const st *)a.x + b * a.x_st + 8 * k8);
                 float f[8];
                 unpack16<DT>(xp[j], f);
-                float t1 = 0.f, t2 = 0.f;
+                float t1 = 0.f;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    t1 += f[e];
-                    t2 = fmaf(f[e], f[e], t2);
-                }
+                for (int e = 0; e < 8; ++e) t1 += f[e];
 #pragma unroll
                 for (int bb = 0; bb < NB; ++bb)
-                    if (bb == b) {
-                        s1[bb] += t1;
-                        s2[bb] += t2;
-                    }
+                    if (bb == b) s1[bb] += t1;
             }
         }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            const float t1 = wave_sum(s1[b]), t2 = wave_sum(s2[b]);
-            if (lane == 0) {
-                red[0][b][w] = t1;
-                red[1][b][w] = t2;
-            }
+            const float t1 = wave_sum(s1[b]);
+            if (lane == 0) red[0][b][w] = t1;
         }
         __syncthreads();
         float mean[NB], rstd[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            float t1 = 0.f, t2 = 0.f;
+            float t1 = 0.f;
 #pragma unroll
-            for (int i = 0; i < LW; ++i) {
-                t1 += red[0][b][i];
-                t2 += red[1][b][i];
-            }
+            for (int i = 0; i < LW; ++i) t1 += red[0][b][i];
             mean[b] = t1 / (float)K;
-            rstd[b] = rsqrtf(fmaxf(t2 / (float)K - mean[b] * mean[b], 0.f) + a.ln_eps);
+            s1[b] = 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < MAXP; ++j) {
+            const int c = tid + LT * j;
+            if (c < np) {
+                const int b = c / K8;
+                float mb = mean[0];
+#pragma unroll
+                for (int bb = 1; bb < NB; ++bb)
+                    if (bb == b) mb = mean[bb];
+                float f[8];
+                unpack16<DT>(xp[j], f);
+                float t2 = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) t2 = fmaf(f[e] - mb, f[e] - mb, t2);
+#pragma unroll
+                for (int bb = 0; bb < NB; ++bb)
+                    if (bb == b) s1[bb] += t2;
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float t2 = wave_sum(s1[b]);
+            if (lane == 0) red[1][b][w] = t2;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            float t2 = 0.f;
+#pragma unroll
+            for (int i = 0; i < LW; ++i) t2 += red[1][b][i];
+            rstd[b] = rsqrtf(t2 / (float)K + a.ln_eps);
         }
 #pragma unroll
         for (int j = 0; j < MAXP; ++j) {
@@ -210,7 +232,7 @@ __global__ __launch_bounds__(LT) void rows_linear_kernel(RowsLinK a) {
         ((st *)a.y)[b_me * a.y_st + n] = from_f32<DT>(v);
         key = ((unsigned long long)order_key(v) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)n);
     }
-    if (a.argmax) {  // block-wide best key per batch row, then one atomic per row
+    if (a.argmax) {  // block-wide best key per batch row, written to the block's own slot
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             unsigned long long k = b_me == b && lane < RPW * NB ? key : 0ull;

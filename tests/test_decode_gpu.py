@@ -158,3 +158,39 @@ def test_decode_graph_replay_advancing_length():
         y_e = fused_hofa_decode(*args[:11], n, sm)
         torch.cuda.synchronize()
         assert torch.equal(y_g, y_e), n
+
+
+def test_workspace_outlives_graph_capture():
+    """A graph captured with a small decode workspace still owns it after an
+    eager call on the same stream needs a larger one: replays must not write
+    into memory the allocator has handed to other tensors."""
+    from outlierneuronattention_amd import _lib, fused_hofa_decode
+    L, short = 40000, 512
+    g, sm, _, _ = make_case(1, 16, L, L, 64, 16, torch.bfloat16, seed=21)
+    out = torch.empty_like(g["state_in"])
+    base = (g["q"], g["k"], g["v"], g["cache_k"], g["cache_v"], g["state_in"], out, g["log_gamma"], g["mix"],
+            g["norm_w"], 16)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    print("workspace vs graph: capture at a short length", flush=True)
+    with torch.cuda.stream(s):
+        fused_hofa_decode(*base, short, sm)  # sizes this stream's workspace for the short plan
+        s.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            y_g = fused_hofa_decode(*base, short, sm)
+        s.synchronize()
+        retired0 = _lib.WORKSPACES.retired_bytes()
+        fused_hofa_decode(*base, L, sm)  # needs a larger workspace on the same stream
+        s.synchronize()
+        assert _lib.WORKSPACES.retired_bytes() > retired0
+        # tensors that would reuse a freed workspace block
+        bystanders = [torch.full((16384,), 0x5A, dtype=torch.uint8, device=DEV) for _ in range(64)]
+        s.synchronize()
+        graph.replay()
+        s.synchronize()
+        y_e = fused_hofa_decode(*base, short, sm)
+        s.synchronize()
+    assert torch.equal(y_g, y_e)
+    for t in bystanders:
+        assert bool((t == 0x5A).all())

@@ -73,6 +73,25 @@ def test_rows_linear_matches_module_chain(dt, B, K, N, ln, gelu, bias, res, scal
     assert torch.equal(idx, out.float().argmax(-1)), (idx, out.float().argmax(-1))
 
 
+@pytest.mark.parametrize("dt,offset", [(torch.float16, 200.0), (torch.bfloat16, 200.0), (torch.float16, -60.0)])
+def test_rows_linear_layernorm_large_offset(dt, offset):
+    """Rows whose mean is far above their spread: the LayerNorm variance is a
+    sum of squared deviations (two passes), so nothing cancels."""
+    from outlierneuronattention_amd.decode_layer import rows_linear
+    g = torch.Generator().manual_seed(11)
+    B, K, N = 4, 1024, 1024
+    x = (torch.randn(B, K, generator=g) + offset).to(DEV, dt)
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(DEV, dt)
+    lnp = (torch.ones(K).to(DEV, dt), torch.zeros(K).to(DEV, dt), 1e-5)
+    ref = _ref_linear(x, w, None, lnp, False, 1.0, 0, None, dt)
+    out = torch.empty(B, N, device=DEV, dtype=dt)
+    print(f"rows_linear LN offset={offset} dt={dt}", flush=True)
+    rows_linear(x, w, out, ln=lnp)
+    torch.cuda.synchronize()
+    err = (out.float() - ref).abs().max().item()
+    assert err <= 1e-2 * ref.abs().max().item(), err
+
+
 def test_rows_linear_in_place_residual_and_errors():
     from outlierneuronattention_amd import _lib
     from outlierneuronattention_amd.decode_layer import rows_linear
