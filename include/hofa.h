@@ -98,6 +98,23 @@ int hofa_decode_plan(const hofa_decode_args_t *args, int32_t *split_k, int32_t *
 
 int hofa_decode(const hofa_decode_args_t *args, void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * hofa_decode_static: hofa_decode without a caller workspace and without any
+ * allocation.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The split-K partials go to a file-scope
+ * device array of HOFA_DECODE_STATIC_SCRATCH_BYTES per GPU, which the library
+ * holds until the process ends; a call whose plan needs more (see
+ * hofa_decode_workspace_bytes) is rejected with HOFA_EWORKSPACE.  At cfg3
+ * (B=4, H=16, d_h=64) a call uses about 0.8 MiB.  Same kernels, split plan and
+ * results as hofa_decode.  Every call on one GPU shares that GPU's array:
+ * calls that may overlap on one GPU (different streams, concurrent threads)
+ * race and must be serialised by the caller.  Nothing in the array needs
+ * initialisation; the caller still passes inputs and outputs.
+ */
+#define HOFA_DECODE_STATIC_SCRATCH_BYTES (8u << 20)
+int hofa_decode_static(const hofa_decode_args_t *args, void *stream);
+
 /* ------------------------------------------------------------------------
  * Outlier pathway of the prefill: causal softmax attention on the first R
  * channels of Q/K against full-width V, mixed into the output.

@@ -17,6 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libhofa.so")
 
 HOFA_F32, HOFA_BF16, HOFA_F16 = 0, 1, 2
+DECODE_STATIC_SCRATCH_BYTES = 8 << 20  # HOFA_DECODE_STATIC_SCRATCH_BYTES of include/hofa.h
 _DTYPE_CODE = {torch.float32: HOFA_F32, torch.bfloat16: HOFA_BF16, torch.float16: HOFA_F16}
 _ERRORS = {-1: "invalid argument", -2: "unsupported configuration", -3: "launch failure", -4: "workspace"}
 
@@ -128,6 +129,7 @@ EXPORTS = [
     ("hofa_decode_plan", ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(ctypes.c_int32),
                                         ctypes.POINTER(ctypes.c_int32)]),
     ("hofa_decode", ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    ("hofa_decode_static", ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]),
     ("hofa_attn_fwd", ctypes.c_int, [ctypes.POINTER(AttnFwdArgs), ctypes.c_void_p]),
     ("hofa_gla_fwd_workspace_bytes", ctypes.c_size_t, [ctypes.POINTER(GlaFwdArgs)]),
     ("hofa_gla_fwd", ctypes.c_int, [ctypes.POINTER(GlaFwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),

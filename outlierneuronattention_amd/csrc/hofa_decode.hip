@@ -23,6 +23,8 @@
 // The kernel boundary orders the partial writes before the merge's reads, so
 // no device-scope fence or counter is needed and the workspace carries no
 // state between calls.
+#include <mutex>
+
 #include "hofa_common.h"
 
 namespace hofa {
@@ -711,4 +713,64 @@ extern "C" int hofa_decode_fused(const hofa_decode_args_t *a, const hofa_decode_
                                                                          p->rope_dtype == p->dtype))),
                  HOFA_EINVAL, "hofa_decode_fused: RoPE tables need cos and sin, rope_rows > 0, f32 or the dtype");
     return run_decode(a, p, workspace, workspace_bytes, stream);
+}
+
+// ------------------------------------------------------------------ allocation-free entry point
+// hofa_decode_static: the split-K partials live in `scratch`, one file-scope
+// device array per GPU, instead of a caller workspace.  Host code never
+// passes the array's name to a kernel (on the host it is a stand-in, not a
+// device address); the address comes from hipGetSymbolAddress, called once
+// per device with that device current, and is kept per device.
+static __device__ __align__(256) unsigned char scratch[HOFA_DECODE_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of this GPU's `scratch` (resolved on first use).
+int scratch_for_stream(hipStream_t stream, void **out) {
+    int dev = -1;
+    if (stream) {
+        HOFA_REQUIRE(hipStreamGetDevice(stream, &dev) == hipSuccess, HOFA_ELAUNCH,
+                     "hofa_decode_static: hipStreamGetDevice failed");
+    } else {
+        HOFA_REQUIRE(hipGetDevice(&dev) == hipSuccess, HOFA_ELAUNCH, "hofa_decode_static: hipGetDevice failed");
+    }
+    HOFA_REQUIRE(dev >= 0 && dev < kMaxDevices, HOFA_EUNSUPPORTED, "hofa_decode_static: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        int cur = -1;
+        HOFA_REQUIRE(hipGetDevice(&cur) == hipSuccess, HOFA_ELAUNCH, "hofa_decode_static: hipGetDevice failed");
+        if (cur != dev)
+            HOFA_REQUIRE(hipSetDevice(dev) == hipSuccess, HOFA_ELAUNCH, "hofa_decode_static: hipSetDevice(%d) failed",
+                         dev);
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (cur != dev) (void)hipSetDevice(cur);
+        HOFA_REQUIRE(e == hipSuccess && ptr, HOFA_ELAUNCH, "hofa_decode_static: hipGetSymbolAddress failed: %s",
+                     hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return HOFA_OK;
+}
+
+}  // namespace
+
+extern "C" int hofa_decode_static(const hofa_decode_args_t *a, void *stream) {
+    int rc = validate(a);
+    if (rc) return rc;
+    int n, t;
+    plan(a, &n, &t);
+    const size_t need = ws_bytes(a, n);
+    HOFA_REQUIRE(need <= (size_t)HOFA_DECODE_STATIC_SCRATCH_BYTES, HOFA_EWORKSPACE,
+                 "hofa_decode_static: this call needs %zu bytes of scratch, more than the %zu-byte static "
+                 "array (B*H=%d heads, %d splits); use hofa_decode with a workspace",
+                 need, (size_t)HOFA_DECODE_STATIC_SCRATCH_BYTES, a->B * a->H, n);
+    void *ptr = nullptr;
+    rc = scratch_for_stream((hipStream_t)stream, &ptr);
+    if (rc) return rc;
+    return run_decode(a, nullptr, ptr, (size_t)HOFA_DECODE_STATIC_SCRATCH_BYTES, stream);
 }
