@@ -174,11 +174,11 @@ def make_prefill_inputs(gen, dev="cuda", B=P_B, T=P_T, H=P_H, D=P_D, R=P_R):
 
 
 def _prefill_call(inp, y):
-    from outlierneuronattention_amd.chunk_gla_inlier import chunk_gla_inlier_fwd
-    from outlierneuronattention_amd.exact_attention import exact_attention
-    chunk_gla_inlier_fwd(inp["q"], inp["k"], inp["v"], inp["lg"], P_R, P_C, mix_g=inp["mix"], gla_scale=inp["gs"],
-                         out=y, g=inp["g"])
-    exact_attention(inp["q"], inp["k"], inp["v"], P_R, math.sqrt(P_D / P_R), inp["mix"], out=y)
+    """The inference module's prefill core: the GLA (general decay g, RMSNorm eps 1e-5 as the
+    reference kernel) in float32, then the outlier attention adding mix * O with one rounding."""
+    from outlierneuronattention_amd.prefill import prefill_fwd
+    prefill_fwd(inp["q"], inp["k"], inp["v"], inp["lg"], P_R, math.sqrt(P_D / P_R), inp["mix"], inp["gs"],
+                g=inp["g"], eps=1e-5, out=y)
 
 
 def bench_prefill(steps: int, warmup: int):

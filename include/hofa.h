@@ -130,6 +130,11 @@ int hofa_decode_static(const hofa_decode_args_t *args, void *stream);
  *   q, k, v, y    [B,H,T,D]
  *   mix           [B,H,T]   strides b, h, t (f32|bf16|f16)
  *   o             optional [B,H,T,D]: O itself (data NULL = not written)
+ *   acc           optional float32 [B,H,T,D] (strides b, h, t; unit last
+ *                 stride, 16-byte aligned rows): y = acc + mix * O, rounded
+ *                 once to the dtype of y (accumulate is then ignored).  With
+ *                 hofa_gla_fwd writing its float32 result to acc, the two
+ *                 pathways meet with a single rounding of the output.
  * lse (optional, float32 [B*H*T], NULL = not written) receives the base-2
  * log-sum-exp of the scaled logits per query row (log2 of the softmax
  * denominator, with logits multiplied by sm_scale*log2(e)).
@@ -147,6 +152,7 @@ typedef struct {
     hofa_view_t y;
     hofa_view_t o;
     float *lse;
+    hofa_view_t acc;
 } hofa_attn_fwd_args_t;
 
 int hofa_attn_fwd(const hofa_attn_fwd_args_t *args, void *stream);
@@ -164,9 +170,11 @@ int hofa_attn_fwd(const hofa_attn_fwd_args_t *args, void *stream);
  *   y = fuse_norm_gate ? (1 - mix) * gla_scale * RMSNorm(Y_I; eps) : Y_I
  *   state_out = S_T
  *
- * Views (element strides; q/k/v/y share one dtype f32|bf16|f16, unit last
+ * Views (element strides; q/k/v share one dtype f32|bf16|f16, unit last
  * stride, 16-byte aligned rows):
- *   q, k, v, y     [B,H,T,D]      strides b, h, t, d
+ *   q, k, v, y     [B,H,T,D]      strides b, h, t, d; y has the dtype of q or
+ *                                 is float32 (the result unrounded, e.g. the
+ *                                 acc input of hofa_attn_fwd)
  *   log_gamma      [B,H,T]        strides b, h, t (f32|bf16|f16); used when g.data is NULL
  *   log_alpha      [H,J]          strides h, j; optional
  *   g              [B,H,T,J] f32  strides b, h, t, j; optional general decay (wins over log_gamma)

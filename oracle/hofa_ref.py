@@ -20,6 +20,9 @@ is listed in the test files that exercise it:
   the scalar-decay special case, and golden vectors (decode recurrence).
 * ``decode_step``  -> golden vectors; equality with the last row of a prefill.
 * ``HOFARef``  -> golden vectors written by the reference's own Train module.
+* ``layer_norm`` / ``gelu``  -> ``nn.LayerNorm`` / ``nn.GELU`` (library routines).
+* ``SubwordLMRef``  -> golden logits written by the reference's own Train
+  ``SubwordLM`` (tests/golden/make_golden_lm.py); decode == last prefill row.
 """
 from __future__ import annotations
 
@@ -62,23 +65,26 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
 # ---------------------------------------------------------------------------
 # Gates (src/HybridOutlierFactorizedAttention.py:67-95, Train :85-113)
 # ---------------------------------------------------------------------------
-def compute_gates(Q, K, gate_w, gate_b, mix_w=None, mix_b=None, fixed_mix=None):
+def compute_gates(Q, K, gate_w, gate_b, mix_w=None, mix_b=None, fixed_mix=None, rd=None):
     """Returns ``gate_logits [B,H,N]`` and ``mix [B,H,N]`` (or ``None``).
 
     The first ``d_h`` input features of each projection multiply Q and the
-    last ``d_h`` multiply K (``W.chunk(2, dim=1)``, :70 / :81).
+    last ``d_h`` multiply K (``W.chunk(2, dim=1)``, :70 / :81).  ``rd``
+    (optional) rounds like a 16-bit module: each einsum, their sum, the sum
+    with the bias and the sigmoid are rounded to the activation dtype.
     """
+    rd = rd or (lambda t: t)
     d = Q.shape[-1]
     wq, wk = gate_w[:, :d], gate_w[:, d:]
-    a = torch.einsum("bhnf,hf->bhn", Q, wq.to(Q.dtype)) + torch.einsum("bhnf,hf->bhn", K, wk.to(Q.dtype))
-    a = a + gate_b.to(Q.dtype).view(1, -1, 1)
+    a = rd(torch.einsum("bhnf,hf->bhn", Q, wq.to(Q.dtype))) + rd(torch.einsum("bhnf,hf->bhn", K, wk.to(Q.dtype)))
+    a = rd(rd(a) + gate_b.to(Q.dtype).view(1, -1, 1))
     mix = None
     if mix_w is not None:
         mq, mk = mix_w[:, :d], mix_w[:, d:]
-        m = torch.einsum("bhnf,hf->bhn", Q, mq.to(Q.dtype)) + torch.einsum("bhnf,hf->bhn", K, mk.to(Q.dtype))
-        mix = torch.sigmoid(m + mix_b.to(Q.dtype).view(1, -1, 1))
+        m = rd(torch.einsum("bhnf,hf->bhn", Q, mq.to(Q.dtype))) + rd(torch.einsum("bhnf,hf->bhn", K, mk.to(Q.dtype)))
+        mix = rd(torch.sigmoid(rd(rd(m) + mix_b.to(Q.dtype).view(1, -1, 1))))
     elif fixed_mix is not None:
-        mix = torch.sigmoid(fixed_mix.to(Q.dtype)).view(1, -1, 1).expand(Q.shape[0], -1, Q.shape[2])
+        mix = rd(torch.sigmoid(fixed_mix.to(Q.dtype))).view(1, -1, 1).expand(Q.shape[0], -1, Q.shape[2])
     return a, mix
 
 
@@ -101,18 +107,49 @@ def decay_from_gates(log_gamma: torch.Tensor, j: int, log_alpha: Optional[torch.
 # (src/exact_attention.py:46-161; Train SDPA :241-259)
 # ---------------------------------------------------------------------------
 def outlier_attention(q_o: torch.Tensor, k_o: torch.Tensor, v: torch.Tensor, sm_scale: float,
-                      causal: bool = True, return_lse: bool = False):
+                      causal: bool = True, return_lse: bool = False, block_rows: int = 2048):
     """``softmax(q_o k_o^T * sm_scale + causal mask) v``; q_o,k_o ``[B,H,N,r]``, v ``[B,H,M,dv]``.
 
     With the module's pre-scaled Q/K (``d_h^{-1/4}`` each) and
     ``sm_scale = sqrt(d_h/r)`` the effective logit is ``q.k/sqrt(r)``
     (src/HybridOutlierFactorizedAttention.py:207).  ``lse`` is the natural-log
-    log-sum-exp of the scaled logits per row.
+    log-sum-exp of the scaled logits per row.  Long inputs are processed per
+    (batch, head) in blocks of ``block_rows`` query rows, which bounds the
+    score matrix held at once; the arithmetic per row is unchanged.
     """
+    B, H, n, _ = q_o.shape
+    m = k_o.shape[2]
+    if B * H * n * m <= (1 << 24):
+        return _attention_rows(q_o, k_o, v, sm_scale, causal, return_lse, None)
+    outs, lses = [], []
+    for b in range(B):
+        ob, lb = [], []
+        for h in range(H):
+            oh, lh = [], []
+            for r0 in range(0, n, block_rows):
+                r1 = min(n, r0 + block_rows)
+                o, l = _attention_rows(q_o[b:b + 1, h:h + 1, r0:r1], k_o[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1],
+                                       sm_scale, causal, True, r0 + (m - n))
+                oh.append(o)
+                lh.append(l)
+            ob.append(torch.cat(oh, 2))
+            lb.append(torch.cat(lh, 2))
+        outs.append(torch.cat(ob, 1))
+        lses.append(torch.cat(lb, 1))
+    out, lse = torch.cat(outs, 0), torch.cat(lses, 0)
+    return (out, lse) if return_lse else out
+
+
+def _attention_rows(q_o, k_o, v, sm_scale, causal, return_lse, row0):
+    """Query rows at key positions ``row0 .. row0 + n - 1`` of the causal
+    softmax attention (``row0 = None``: the last query row sits at the last key)."""
     s = torch.matmul(q_o, k_o.transpose(-1, -2)) * sm_scale
     if causal:
         n, m = s.shape[-2], s.shape[-1]
-        mask = torch.ones(n, m, dtype=torch.bool).tril(diagonal=m - n)
+        if row0 is None:
+            mask = torch.ones(n, m, dtype=torch.bool).tril(diagonal=m - n)
+        else:
+            mask = torch.arange(m).view(1, m) <= (row0 + torch.arange(n)).view(n, 1)
         s = s.masked_fill(~mask, float("-inf"))
     lse = torch.logsumexp(s, dim=-1)
     p = torch.exp(s - lse.unsqueeze(-1))
@@ -257,8 +294,15 @@ class HOFARef:
 
     def __init__(self, state: dict, d_model: int, num_heads: int, r: int, rope_base: float = 10000.0,
                  use_rope: bool = True, attention_scale: float = 1.0, chunk: int = 64,
-                 dtype=torch.float64):
+                 dtype=torch.float64, act_dtype=None, rope_f32_tables: bool = False):
+        self.act = act_dtype
+        self.rope_f32 = rope_f32_tables
         self.p = {kk: vv.detach().to(dtype) for kk, vv in state.items()}
+        if act_dtype is not None:  # weights enter the 16-bit ops rounded (a cast module or autocast)
+            for kk in ("W_q.weight", "W_k.weight", "W_v.weight", "out_proj.weight", "gate_proj.weight",
+                       "gate_proj.bias", "mix_proj.weight", "mix_proj.bias"):
+                if kk in self.p:
+                    self.p[kk] = self.p[kk].to(act_dtype).to(dtype)
         self.D, self.H = d_model, num_heads
         self.dh = d_model // num_heads
         self.r, self.j = r, self.dh - r
@@ -268,28 +312,44 @@ class HOFARef:
         self.dtype = dtype
 
     # -- shared pieces ----------------------------------------------------
+    def _rd(self, t):
+        """Round to the activation dtype (identity without one)."""
+        return t if self.act is None else t.to(self.act).to(self.dtype)
+
     def _qkv(self, x):
         """Projections (Infer :100-104, Train :132-137): Q,K scaled by d_h^{-1/4}."""
         B, N, _ = x.shape
-        x = x.to(self.dtype)
+        rd = self._rd
+        x = rd(x.to(self.dtype))
         s = self.dh ** 0.25
-        Q = (x @ self.p["W_q.weight"].T / s).view(B, N, self.H, self.dh).transpose(1, 2)
-        K = (x @ self.p["W_k.weight"].T / s).view(B, N, self.H, self.dh).transpose(1, 2)
-        V = (x @ self.p["W_v.weight"].T).view(B, N, self.H, self.dh).transpose(1, 2)
+        Q = rd(rd(x @ self.p["W_q.weight"].T) / s).view(B, N, self.H, self.dh).transpose(1, 2)
+        K = rd(rd(x @ self.p["W_k.weight"].T) / s).view(B, N, self.H, self.dh).transpose(1, 2)
+        V = rd(x @ self.p["W_v.weight"].T).view(B, N, self.H, self.dh).transpose(1, 2)
         return Q, K, V
 
     def _gates(self, Q, K):
+        kw = {} if self.act is None else {"rd": self._rd}
         return compute_gates(Q, K, self.p["gate_proj.weight"], self.p["gate_proj.bias"],
                              self.p.get("mix_proj.weight"), self.p.get("mix_proj.bias"),
-                             self.p.get("fixed_mix"))
+                             self.p.get("fixed_mix"), **kw)
 
     def _rope(self, n0, n1):
         cos, sin = rope_tables(self.r, n1, self.rope_base)
-        return cos[n0:n1].to(self.dtype), sin[n0:n1].to(self.dtype)
+        cos, sin = cos[n0:n1].to(self.dtype), sin[n0:n1].to(self.dtype)
+        if self.rope_f32:
+            return cos, sin
+        return self._rd(cos), self._rd(sin)
+
+    def _apply_rope(self, x, cos, sin):
+        if self.act is None:
+            return apply_rope(x, cos, sin)
+        if self.rope_f32:
+            return self._rd(apply_rope(x, cos, sin))
+        return self._rd(self._rd(x * cos) + self._rd(rotate_half(x) * sin))
 
     def _out(self, Y):
         B, H, N, d = Y.shape
-        return Y.transpose(1, 2).reshape(B, N, H * d) @ self.p["out_proj.weight"].T
+        return self._rd(Y.transpose(1, 2).reshape(B, N, H * d) @ self.p["out_proj.weight"].T)
 
     def _log_alpha(self):
         return self.p.get("log_alpha")
@@ -307,15 +367,15 @@ class HOFARef:
         Q, K, V = self._qkv(x)
         N = x.shape[1]
         a, mix = self._gates(Q, K)
-        log_gamma = F.logsigmoid(-a)                                     # Infer :177
+        log_gamma = self._rd(F.logsigmoid(-a))                           # Infer :177
         if self.use_rope:
             cos, sin = self._rope(0, N)
-            Q = torch.cat([apply_rope(Q[..., :self.r], cos, sin), Q[..., self.r:]], -1)
-            K = torch.cat([apply_rope(K[..., :self.r], cos, sin), K[..., self.r:]], -1)
+            Q = torch.cat([self._apply_rope(Q[..., :self.r], cos, sin), Q[..., self.r:]], -1)
+            K = torch.cat([self._apply_rope(K[..., :self.r], cos, sin), K[..., self.r:]], -1)
         g = decay_from_gates(log_gamma, self.j, self._log_alpha())
         sm = (self.dh / self.r) ** 0.5 * sm_extra
         Y, S = hofa_core(Q, K, V, g, mix, self._gla_scale(), self.r, sm, eps=eps, chunk=self.chunk)
-        out = self._out(Y)
+        out = self._out(self._rd(Y))
         if return_state:
             return out, (K[..., :self.r].contiguous(), V.contiguous()), S
         return out
@@ -332,8 +392,8 @@ class HOFARef:
         pos = 0 if cache_O is None else cache_O[0].shape[2]
         if self.use_rope:
             cos, sin = self._rope(pos, pos + 1)
-            Q = torch.cat([apply_rope(Q[..., :self.r], cos, sin), Q[..., self.r:]], -1)
-            K = torch.cat([apply_rope(K[..., :self.r], cos, sin), K[..., self.r:]], -1)
+            Q = torch.cat([self._apply_rope(Q[..., :self.r], cos, sin), Q[..., self.r:]], -1)
+            K = torch.cat([self._apply_rope(K[..., :self.r], cos, sin), K[..., self.r:]], -1)
         if cache_O is None:
             cache_O = (K[..., :self.r], V)
         else:
@@ -342,8 +402,92 @@ class HOFARef:
             state = torch.zeros(B, self.H, self.j, self.dh, dtype=self.dtype)
         la = self._log_alpha()
         y, S = decode_step(Q[:, :, 0], K[:, :, 0], V[:, :, 0], cache_O[0], cache_O[1], cache_O[0].shape[2],
-                           state, F.logsigmoid(-a)[:, :, 0], mix[:, :, 0],
+                           state, self._rd(F.logsigmoid(-a))[:, :, 0], mix[:, :, 0],
                            self._gla_scale().reshape(self.H, self.dh), self.r,
                            (self.dh / self.r) ** 0.5, eps=eps,
                            log_alpha=None if la is None else la.reshape(self.H, self.j))
-        return self._out(y.unsqueeze(2)), cache_O, S
+        return self._out(self._rd(y).unsqueeze(2)), cache_O, S
+
+
+# ---------------------------------------------------------------------------
+# Language-model stack (src/HybridOutlierFactorizedAttention.py:425-513,
+# Train src/HybridOutlierFactorizedAttentionTrain.py:441-502)
+# ---------------------------------------------------------------------------
+def layer_norm(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """``nn.LayerNorm(d)`` (biased variance, default eps 1e-5), as ``ln_1``/``ln_2``/``ln_f`` (:427,429,468)."""
+    mu = x.mean(-1, keepdim=True)
+    var = (x - mu).pow(2).mean(-1, keepdim=True)
+    return (x - mu) * torch.rsqrt(var + eps) * w + b
+
+
+def gelu(x: torch.Tensor) -> torch.Tensor:
+    """``nn.GELU()`` (erf form, the default) of the block MLP (:432)."""
+    return 0.5 * x * (1.0 + torch.erf(x * (1.0 / math.sqrt(2.0))))
+
+
+class SubwordLMRef:
+    """Functional restatement of ``SubwordLM`` / ``TransformerBlock`` on a state
+    dict with the reference names: token embedding tied to ``lm_head``
+    (:471), per layer ``x + attn(ln_1(x))`` then ``x + mlp(ln_2(x))`` with a
+    4x GELU MLP (:436-451), ``ln_f`` and the LM head (:476-483).  Per-layer
+    ``r`` comes from ``r_list`` (:459-467).  The attention of each layer is
+    ``HOFARef`` (hybrid path, 0 < r < d_h).  ``attn_eps`` is the inlier
+    RMSNorm epsilon used in prefill.
+    """
+
+    def __init__(self, state: dict, d_model: int, num_heads: int, r_list, rope_base: float = 10000.0,
+                 attn_eps: float = FP32_EPS, dtype=torch.float64, act_dtype=None):
+        self.dtype = dtype
+        self.act = act_dtype
+        self.attn_eps = attn_eps
+        self.emb = state["lm_head.weight"].detach().to(dtype)
+        self.lnf = (state["ln_f.weight"].detach().to(dtype), state["ln_f.bias"].detach().to(dtype))
+        self.layers = []
+        for i, r in enumerate(r_list):
+            pre = f"layers.{i}."
+            sub = {k[len(pre):]: v for k, v in state.items() if k.startswith(pre)}
+            attn = HOFARef({k[len("attn."):]: v for k, v in sub.items() if k.startswith("attn.")}, d_model,
+                           num_heads, r, rope_base=rope_base, dtype=dtype, act_dtype=act_dtype)
+            t = {k: v.detach().to(dtype) for k, v in sub.items() if not k.startswith("attn.")}
+            self.layers.append((attn, t))
+
+    def _rd(self, t):
+        return t if self.act is None else t.to(self.act).to(self.dtype)
+
+    def _ln(self, x, w, b):
+        return self._rd(layer_norm(x, w, b))
+
+    def _mlp(self, t, x):
+        h = self._rd(gelu(self._rd(x @ t["mlp.0.weight"].T + t["mlp.0.bias"])))
+        return self._rd(h @ t["mlp.2.weight"].T + t["mlp.2.bias"])
+
+    def _head(self, x):
+        return self._rd(self._ln(x, *self.lnf) @ self.emb.T)
+
+    def forward(self, ids: torch.Tensor, return_state: bool = False, last_only: bool = False):
+        """Logits ``[B, N, vocab]`` (``last_only``: ``[B, 1, vocab]``); with
+        ``return_state`` also the per-layer caches and GLA states (:476-483)."""
+        x = self.emb[ids]
+        caches, states = [], []
+        for attn, t in self.layers:
+            a, cache, S = attn.forward(self._ln(x, t["ln_1.weight"], t["ln_1.bias"]), eps=self.attn_eps,
+                                       return_state=True)
+            caches.append(cache)
+            states.append(S)
+            x = self._rd(x + a)
+            x = self._rd(x + self._mlp(t, self._ln(x, t["ln_2.weight"], t["ln_2.bias"])))
+        logits = self._head(x[:, -1:] if last_only else x)
+        return (logits, caches, states) if return_state else logits
+
+    def forward_step(self, ids: torch.Tensor, caches, states):
+        """One token ``ids [B, 1]`` per sequence on caches holding exactly the
+        past rows (:446-451, :485-513); returns ``(logits [B,1,vocab], caches, states)``."""
+        x = self.emb[ids]
+        new_c, new_s = [], []
+        for (attn, t), c, S in zip(self.layers, caches, states):
+            a, c, S = attn.forward_step(self._ln(x, t["ln_1.weight"], t["ln_1.bias"]), c, S)
+            new_c.append(c)
+            new_s.append(S)
+            x = self._rd(x + a)
+            x = self._rd(x + self._mlp(t, self._ln(x, t["ln_2.weight"], t["ln_2.bias"])))
+        return self._head(x), new_c, new_s

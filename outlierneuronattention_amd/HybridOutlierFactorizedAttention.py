@@ -6,9 +6,10 @@ signatures, return values and cache / state layout as the reference class
 ``SubwordLM`` (:425-513).  The hybrid path (0 < r < d_head) runs on the gfx950
 kernels of this package:
 
-* prefill: ``chunk_gla_inlier_fwd`` writes ``(1 - mix) * gla_scale *
-  RMSNorm(GLA)``, then ``exact_attention`` adds ``mix * softmax-attention``
-  (the reference's two-kernel order, :201-208);
+* prefill: ``chunk_gla_inlier_fwd`` computes ``(1 - mix) * gla_scale *
+  RMSNorm(GLA)`` and ``exact_attention`` adds ``mix * softmax-attention``
+  (the reference's two-kernel order, :201-208), the GLA part passed on in
+  float32 so the output is rounded once (``prefill.prefill_fwd``);
 * decode: ``fused_hofa_decode`` (split-K cache streaming + state update).
 
 Projections, gate einsums and RoPE are PyTorch GEMM/elementwise work as in
@@ -31,6 +32,7 @@ from .config import ModelConfig
 from .exact_attention import exact_attention
 from .hofa_decode import fused_hofa_decode
 from .modules import RotaryEmbedding, apply_rotary_pos_emb
+from .prefill import prefill_fwd
 
 _ATTN_WIDTHS = (16, 32, 64)
 # RMSNorm epsilon of the inlier norm in prefill and decode alike: the one of
@@ -163,10 +165,9 @@ class HybridOutlierFactorizedAttention(nn.Module):
             K_cache = K[..., :self.r].contiguous()
             V_cache = V.contiguous()
         log_alpha = self.log_alpha if self.learnable_alpha else None
-        Y, states_out = chunk_gla_inlier_fwd(Q, K, V, log_gamma, self.r, self.chunk_size, log_alpha=log_alpha,
-                                             mix_g=mix_g, gla_scale=self.gla_scale, eps=_NORM_EPS)
         sm_scale = (self.d_head / self.r) ** 0.5
-        exact_attention(Q, K, V, self.r, sm_scale, mix_g.squeeze(-1), out=Y)
+        Y, states_out = prefill_fwd(Q, K, V, log_gamma, self.r, sm_scale, mix_g.squeeze(-1), self.gla_scale,
+                                    log_alpha=log_alpha, eps=_NORM_EPS)
         Y_out = self._merge(Y, dtype_in)
         if return_state:
             state_I = states_out[:, :, :self.j, :self.d_head].contiguous()

@@ -49,7 +49,7 @@ class AttnFwdArgs(ctypes.Structure):
                 ("R", ctypes.c_int32), ("sm_scale", ctypes.c_float), ("accumulate", ctypes.c_int32),
                 ("reserved", ctypes.c_int32),
                 ("q", View), ("k", View), ("v", View), ("mix", View), ("y", View), ("o", View),
-                ("lse", ctypes.c_void_p)]
+                ("lse", ctypes.c_void_p), ("acc", View)]
 
 
 class GlaFwdArgs(ctypes.Structure):

@@ -24,8 +24,9 @@ from __future__ import annotations
 
 import torch
 
-from .chunk_gla_inlier import chunk_gla_inlier_bwd, chunk_gla_inlier_fwd, chunk_states_numel
-from .exact_attention import exact_attention, exact_attention_bwd
+from .chunk_gla_inlier import chunk_gla_inlier_bwd, chunk_states_numel
+from .exact_attention import exact_attention_bwd
+from .prefill import prefill_fwd
 
 FP32_EPS = float(torch.finfo(torch.float32).eps)
 
@@ -59,14 +60,11 @@ class _HOFACore(torch.autograd.Function):
             n = torch.empty(B, H, T, D, dtype=v.dtype, device=dev)
             rstd = torch.empty(B * H * T, dtype=torch.float32, device=dev)
             cs = torch.empty(chunk_states_numel(B, H, T, D, J), dtype=torch.int16, device=dev)
-        chunk_gla_inlier_fwd(q, k, v, log_gamma, r, 64, log_alpha=log_alpha, mix_g=mix_eff, gla_scale=gla_scale,
-                             out=y, eps=FP32_EPS, chunk_states=cs, n_out=n, rstd=rstd)
-        if r > 0:
-            if train and mix is not None:
-                o = torch.empty(B, H, T, D, dtype=v.dtype, device=dev)
-                lse = torch.empty(B * H * T, dtype=torch.float32, device=dev)
-            exact_attention(q if q_o is None else q_o, k if k_o is None else k_o, v, r, sm_scale, mix_eff, out=y,
-                            o=o, lse=lse)
+        if r > 0 and train and mix is not None:
+            o = torch.empty(B, H, T, D, dtype=v.dtype, device=dev)
+            lse = torch.empty(B * H * T, dtype=torch.float32, device=dev)
+        prefill_fwd(q, k, v, log_gamma, r, sm_scale, mix_eff, gla_scale, log_alpha=log_alpha, eps=FP32_EPS,
+                    q_o=q_o, k_o=k_o, out=y, chunk_states=cs, n_out=n, rstd=rstd, o=o, lse=lse)
         if train:
             ctx.save_for_backward(q_o, k_o, q, k, v, log_gamma, log_alpha, mix, gla_scale, n, rstd, cs, o, lse)
             ctx.r, ctx.sm_scale = r, sm_scale

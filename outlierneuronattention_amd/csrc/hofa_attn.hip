@@ -30,6 +30,8 @@ struct AttnFwdK {
     const void *q, *k, *v, *mix;
     void *y, *o;
     float *lse;
+    const float *acc;  // optional f32 partial: y = acc + mix * O
+    int64_t a_sb, a_sh, a_st;
     int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st;
     int64_t y_sb, y_sh, y_st, o_sb, o_sh, o_st;
     int64_t m_sb, m_sh, m_st;
@@ -233,6 +235,7 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
     const float mixv = a.mix ? load_any(a.mix, a.mix_dt, b * a.m_sb + h * a.m_sh + (int64_t)qrow * a.m_st) : 1.f;
     in_t *yr = (in_t *)a.y + b * a.y_sb + h * a.y_sh + (int64_t)qrow * a.y_st;
     in_t *orow = a.o ? (in_t *)a.o + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_st : nullptr;
+    const float *arow = a.acc ? a.acc + b * a.a_sb + h * a.a_sh + (int64_t)qrow * a.a_st : nullptr;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -244,7 +247,11 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
                 ov[e] = o[mb][4 * g + e] * inv;
                 yv[e] = mixv * ov[e];
             }
-            if (a.accumulate) {
+            if (arow) {
+                const f32x4 p = *(const f32x4 *)(arow + dv);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) yv[e] += p[e];
+            } else if (a.accumulate) {
                 if constexpr (DT == HOFA_F32) {
                     const f32x4 p = *(const f32x4 *)(yr + dv);
 #pragma unroll
@@ -316,12 +323,16 @@ extern "C" int hofa_attn_fwd(const hofa_attn_fwd_args_t *a, void *stream) {
                  HOFA_EINVAL, "hofa_attn_fwd: q/k/v/y/o need unit last stride and 16-byte aligned rows");
     HOFA_REQUIRE(!a->mix.data || a->mix.dtype == HOFA_F32 || a->mix.dtype == HOFA_BF16 || a->mix.dtype == HOFA_F16,
                  HOFA_EINVAL, "hofa_attn_fwd: bad mix dtype");
+    HOFA_REQUIRE(!a->acc.data || (a->acc.dtype == HOFA_F32 && rows_ok(a->acc, 4)), HOFA_EINVAL,
+                 "hofa_attn_fwd: acc must be float32 with unit last stride and 16-byte aligned rows");
     HOFA_REQUIRE((int64_t)(a->T + 2 * BN) * a->k.stride[2] * es < (1ll << 31) &&
                      (int64_t)(a->T + 2 * BN) * a->v.stride[2] * es < (1ll << 31),
                  HOFA_EUNSUPPORTED, "hofa_attn_fwd: one head's K/V rows must span less than 2 GiB");
     AttnFwdK k{};
     k.q = a->q.data; k.k = a->k.data; k.v = a->v.data; k.mix = a->mix.data;
     k.y = (void *)a->y.data; k.o = (void *)a->o.data; k.lse = a->lse;
+    k.acc = (const float *)a->acc.data;
+    k.a_sb = a->acc.stride[0]; k.a_sh = a->acc.stride[1]; k.a_st = a->acc.stride[2];
     k.q_sb = a->q.stride[0]; k.q_sh = a->q.stride[1]; k.q_st = a->q.stride[2];
     k.k_sb = a->k.stride[0]; k.k_sh = a->k.stride[1]; k.k_st = a->k.stride[2];
     k.v_sb = a->v.stride[0]; k.v_sh = a->v.stride[1]; k.v_st = a->v.stride[2];

@@ -196,21 +196,29 @@ __device__ void state_block_pro(const DecodeKArgs &a, int bh) {
         s_v[i] = to_f32<DT>(vp[i * a.v_sd]);
     }
     __syncthreads();
-    if (tid < 64) {  // gate and mix logits on the pre-RoPE q, k, rounded as the module's 16-bit einsums
+    if (tid < 64) {  // gate and mix logits on the pre-RoPE q, k, rounded as the module's 16-bit ops
         const st *gw = (const st *)a.gate_w + h * 2 * D;
         const st *mw = a.mix_w ? (const st *)a.mix_w + h * 2 * D : nullptr;
-        float g = 0.f, m = 0.f;
+        float gq = 0.f, gk = 0.f, mq = 0.f, mk = 0.f;
         for (int d = lane; d < D; d += 64) {
-            g = fmaf(s_q[d], to_f32<DT>(gw[d]), fmaf(s_k[d], to_f32<DT>(gw[D + d]), g));
-            if (mw) m = fmaf(s_q[d], to_f32<DT>(mw[d]), fmaf(s_k[d], to_f32<DT>(mw[D + d]), m));
+            gq = fmaf(s_q[d], to_f32<DT>(gw[d]), gq);
+            gk = fmaf(s_k[d], to_f32<DT>(gw[D + d]), gk);
+            if (mw) {
+                mq = fmaf(s_q[d], to_f32<DT>(mw[d]), mq);
+                mk = fmaf(s_k[d], to_f32<DT>(mw[D + d]), mk);
+            }
         }
-        g = wave_sum(g);
-        m = wave_sum(m);
-        if (lane == 0) {
-            const float gl = rnd_st<DT>(g + to_f32<DT>(((const st *)a.gate_b)[h]));
+        gq = wave_sum(gq);
+        gk = wave_sum(gk);
+        mq = wave_sum(mq);
+        mk = wave_sum(mk);
+        if (lane == 0) {  // each einsum rounded, then their sum, then the sum with the bias
+            const float gl = rnd_st<DT>(rnd_st<DT>(rnd_st<DT>(gq) + rnd_st<DT>(gk)) +
+                                        to_f32<DT>(((const st *)a.gate_b)[h]));
             const float ng = -gl;
             s_gate[0] = rnd_st<DT>(fminf(ng, 0.f) - log1pf(expf(-fabsf(ng))));
-            const float ml = mw ? rnd_st<DT>(m + to_f32<DT>(((const st *)a.mix_b)[h]))
+            const float ml = mw ? rnd_st<DT>(rnd_st<DT>(rnd_st<DT>(mq) + rnd_st<DT>(mk)) +
+                                             to_f32<DT>(((const st *)a.mix_b)[h]))
                                 : to_f32<DT>(((const st *)a.fixed_mix)[h]);
             s_gate[1] = rnd_st<DT>(1.f / (1.f + expf(-ml)));
         }

@@ -301,31 +301,36 @@ __global__ __launch_bounds__(64) void decode_prologue_kernel(PrologueK a) {
     st *kr = qr + HD;
     const st *vr = qr + 2 * HD;
     float q[PL], k[PL];
-    float g = 0.f, m = 0.f;
+    float gq = 0.f, gk = 0.f, mq = 0.f, mk = 0.f;
 #pragma unroll
     for (int p = 0; p < PL; ++p) {
         const int d = lane + 64 * p;
         q[p] = to_f32<DT>(qr[d]);
         k[p] = to_f32<DT>(kr[d]);
         const st *gw = (const st *)a.gate_w + h * 2 * D;
-        g = fmaf(q[p], to_f32<DT>(gw[d]), fmaf(k[p], to_f32<DT>(gw[D + d]), g));
+        gq = fmaf(q[p], to_f32<DT>(gw[d]), gq);
+        gk = fmaf(k[p], to_f32<DT>(gw[D + d]), gk);
         if (a.mix_w) {
             const st *mw = (const st *)a.mix_w + h * 2 * D;
-            m = fmaf(q[p], to_f32<DT>(mw[d]), fmaf(k[p], to_f32<DT>(mw[D + d]), m));
+            mq = fmaf(q[p], to_f32<DT>(mw[d]), mq);
+            mk = fmaf(k[p], to_f32<DT>(mw[D + d]), mk);
         }
     }
-    g = wave_sum(g);
-    m = wave_sum(m);
+    gq = wave_sum(gq);
+    gk = wave_sum(gk);
+    mq = wave_sum(mq);
+    mk = wave_sum(mk);
     const int64_t pos = *a.pos;
     if (lane == 0) {
-        // 16-bit logits as the module's einsums produce them, then
-        // log_gamma = logsigmoid(-gate) and mix = sigmoid(.) rounded likewise
-        const float gl = rnd<DT>(g + to_f32<DT>(((const st *)a.gate_b)[h]));
+        // 16-bit logits as the module's ops produce them: each einsum rounded,
+        // then their sum, then the sum with the bias; log_gamma =
+        // logsigmoid(-gate) and mix = sigmoid(.) rounded likewise
+        const float gl = rnd<DT>(rnd<DT>(rnd<DT>(gq) + rnd<DT>(gk)) + to_f32<DT>(((const st *)a.gate_b)[h]));
         const float ng = -gl;
         const float lg = fminf(ng, 0.f) - log1pf(expf(-fabsf(ng)));
         a.log_gamma[bh] = rnd<DT>(lg);
         float ml;
-        if (a.mix_w) ml = rnd<DT>(m + to_f32<DT>(((const st *)a.mix_b)[h]));
+        if (a.mix_w) ml = rnd<DT>(rnd<DT>(rnd<DT>(mq) + rnd<DT>(mk)) + to_f32<DT>(((const st *)a.mix_b)[h]));
         else ml = to_f32<DT>(((const st *)a.fixed_mix)[h]);
         a.mix[bh] = rnd<DT>(1.f / (1.f + expf(-ml)));
     }

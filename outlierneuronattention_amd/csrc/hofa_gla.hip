@@ -230,12 +230,24 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
             }
     }
     if (tq >= a.T) return;
-    in_t *yr = (in_t *)a.y + b * a.y_sb + h * a.y_sh + (int64_t)tq * a.y_st;
+    const int64_t yo = b * a.y_sb + h * a.y_sh + (int64_t)tq * a.y_st;
+    if (a.y_f32) {  // unrounded result for a later single rounding (hofa_attn_fwd acc)
+        float *yr = (float *)a.y + yo;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-            store4<DT>(yr + 32 * mb + 8 * g + 4 * hi, y[mb][4 * g], y[mb][4 * g + 1], y[mb][4 * g + 2], y[mb][4 * g + 3]);
+            for (int g = 0; g < 4; ++g)
+                store4<HOFA_F32>(yr + 32 * mb + 8 * g + 4 * hi, y[mb][4 * g], y[mb][4 * g + 1], y[mb][4 * g + 2],
+                                 y[mb][4 * g + 3]);
+    } else {
+        in_t *yr = (in_t *)a.y + yo;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                store4<DT>(yr + 32 * mb + 8 * g + 4 * hi, y[mb][4 * g], y[mb][4 * g + 1], y[mb][4 * g + 2],
+                           y[mb][4 * g + 3]);
+    }
 }
 
 // ------------------------------------------------------------------ host
@@ -271,12 +283,13 @@ int validate(const hofa_gla_fwd_args_t *a) {
                  "hofa_gla_fwd: inlier width J=%d must be a positive multiple of 16", J);
     const int dt = a->q.dtype;
     HOFA_REQUIRE(dt == HOFA_F32 || dt == HOFA_BF16 || dt == HOFA_F16, HOFA_EINVAL, "hofa_gla_fwd: bad dtype %d", dt);
-    HOFA_REQUIRE(a->k.dtype == dt && a->v.dtype == dt && a->y.dtype == dt, HOFA_EINVAL,
-                 "hofa_gla_fwd: q, k, v and y must share one dtype");
+    HOFA_REQUIRE(a->k.dtype == dt && a->v.dtype == dt && (a->y.dtype == dt || a->y.dtype == HOFA_F32), HOFA_EINVAL,
+                 "hofa_gla_fwd: q, k and v must share one dtype; y has it too or is float32");
     HOFA_REQUIRE(a->q.data && a->k.data && a->v.data && a->y.data && a->state_out.data, HOFA_EINVAL,
                  "hofa_gla_fwd: NULL tensor pointer");
     const int es = elem_bytes(dt);
-    HOFA_REQUIRE(rows_ok(a->q, es) && rows_ok(a->k, es) && rows_ok(a->v, es) && rows_ok(a->y, es), HOFA_EINVAL,
+    HOFA_REQUIRE(rows_ok(a->q, es) && rows_ok(a->k, es) && rows_ok(a->v, es) && rows_ok(a->y, elem_bytes(a->y.dtype)),
+                 HOFA_EINVAL,
                  "hofa_gla_fwd: q/k/v/y need unit last stride and 16-byte aligned rows");
     HOFA_REQUIRE((a->R * es) % 16 == 0, HOFA_EINVAL, "hofa_gla_fwd: the inlier columns must start 16-byte aligned");
     HOFA_REQUIRE(a->g.data || a->log_gamma.data, HOFA_EINVAL, "hofa_gla_fwd: give log_gamma or g");
@@ -367,6 +380,7 @@ extern "C" int hofa_gla_fwd(const hofa_gla_fwd_args_t *a, void *workspace, size_
     k.nc = (a->T + C - 1) / C;
     k.key_col0 = a->R;
     k.fuse = a->fuse_norm_gate;
+    k.y_f32 = a->y.dtype == HOFA_F32 && a->q.dtype != HOFA_F32;
     k.eps = a->eps;
     const int J = a->D - a->R;
     hipStream_t s = (hipStream_t)stream;

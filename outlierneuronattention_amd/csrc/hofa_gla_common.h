@@ -113,6 +113,7 @@ struct GlaK {
     int nplanes;        // 2: hi/lo of S^T [D][J]; 4: also hi/lo of S [J][D]
     int pad_rows;       // state_out rows J .. J+pad_rows-1 to write as zeros
     int fuse;
+    int y_f32;          // y is float32 (unrounded result) rather than the input dtype
     float eps;
 };
 

@@ -15,7 +15,7 @@ import torch
 from . import _lib
 
 
-def attn_fwd_args(q, k, v, r, sm_scale, mix_g, out, accumulate, o=None, lse=None):
+def attn_fwd_args(q, k, v, r, sm_scale, mix_g, out, accumulate, o=None, lse=None, acc=None):
     B, H, T, Dq = q.shape
     D = v.shape[-1]
     r = int(r)
@@ -38,25 +38,33 @@ def attn_fwd_args(q, k, v, r, sm_scale, mix_g, out, accumulate, o=None, lse=None
         if lse.dtype != torch.float32 or not lse.is_contiguous() or lse.numel() != B * H * T:
             raise _lib.HofaError("lse must be a contiguous float32 tensor of B*H*T elements")
         a.lse = lse.data_ptr()
+    if acc is not None:
+        _lib.expect_shape(acc, (B, H, T, D), "acc")
+        if acc.dtype != torch.float32:
+            raise _lib.HofaError("acc must be float32")
+        a.acc = _lib.view(acc)
     return a
 
 
 def exact_attention(q, k, v, r: int, sm_scale: float, mix_g: Optional[torch.Tensor], out=None, split_k=None,
-                    o: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None):
+                    o: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
+                    acc: Optional[torch.Tensor] = None):
     """Causal softmax attention on ``q[..., :r] k[..., :r]^T * sm_scale`` against
     full-width ``v``, mixed into ``out``: ``out += mix_g * O``.  Without ``out``
     a fresh tensor holding ``mix_g * O`` is returned (the reference starts from
     zeros, src/exact_attention.py:165-166).  ``split_k`` is accepted for
     signature compatibility and unused, as in the reference.  Optional ``o``
     receives O itself and ``lse`` (float32, B*H*T) the base-2 log-sum-exp of
-    the logits scaled by ``sm_scale*log2(e)``.
+    the logits scaled by ``sm_scale*log2(e)``.  ``acc`` (float32, the shape of
+    ``out``) replaces the prior contents of ``out``: ``out = acc + mix_g * O``,
+    rounded once (used with a float32 result of ``chunk_gla_inlier_fwd``).
     """
-    _lib.require_gpu(q, k, v, mix_g, out, o, lse)
+    _lib.require_gpu(q, k, v, mix_g, out, o, lse, acc)
     lib = _lib.load()
     accumulate = out is not None
     if out is None:
         out = torch.empty(*q.shape[:3], v.shape[-1], dtype=v.dtype, device=v.device)
-    a = attn_fwd_args(q, k, v, r, sm_scale, mix_g, out, accumulate, o, lse)
+    a = attn_fwd_args(q, k, v, r, sm_scale, mix_g, out, accumulate, o, lse, acc)
     _lib.check(lib.hofa_attn_fwd(ctypes.byref(a), _lib.stream_handle(q.device)), "exact_attention")
     return out
 

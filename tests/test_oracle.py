@@ -221,3 +221,78 @@ def test_core_backward_matches_finite_differences():
         return ref.hofa_core(q, k, v, g, mix, gs, r, 1.3, eps=1e-6, chunk=4)[0]
 
     assert torch.autograd.gradcheck(f, (q, k, v, g, mix, gs), eps=1e-6, atol=1e-7, rtol=1e-5)
+
+
+# ---------------------------------------------------------------- language-model stack
+def _lm_golden(name):
+    import numpy as np
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", f"hofa_lm_{name}.npz"))
+    d_model, H, layers, vocab, B, N, alpha = (int(v) for v in z["meta"])
+    params = {k[len("param."):]: torch.from_numpy(z[k].copy()) for k in z.files if k.startswith("param.")}
+    return dict(d_model=d_model, H=H, r_list=[int(v) for v in z["r_list"]], params=params,
+                ids=torch.from_numpy(z["ids"].copy()), logits=torch.from_numpy(z["logits"].copy()))
+
+
+LM_CASES = ["2l_r16", "3l_rlist_alpha"]
+
+
+@pytest.mark.parametrize("name", LM_CASES)
+def test_lm_matches_reference_golden(name):
+    """SubwordLMRef against logits written by the reference's own SubwordLM."""
+    g = _lm_golden(name)
+    m = ref.SubwordLMRef(g["params"], g["d_model"], g["H"], g["r_list"])
+    logits = m.forward(g["ids"])
+    torch.testing.assert_close(logits.float(), g["logits"], rtol=1e-4, atol=1e-4)
+
+
+def test_layer_norm_and_gelu_match_torch_modules():
+    x = torch.randn(3, 5, 64, dtype=torch.float64) * 3 + 7
+    ln = torch.nn.LayerNorm(64).double()
+    with torch.no_grad():
+        ln.weight.normal_()
+        ln.bias.normal_()
+    torch.testing.assert_close(ref.layer_norm(x, ln.weight, ln.bias), ln(x).detach())
+    torch.testing.assert_close(ref.gelu(x - 7), torch.nn.GELU()(x - 7))
+
+
+def test_lm_decode_steps_equal_last_prefill_rows():
+    """forward_step over cached prefill state == last row of a longer prefill
+    (the reference's own check, benchmarks/validate_kernels.py:312-337)."""
+    g = _lm_golden("3l_rlist_alpha")
+    m = ref.SubwordLMRef(g["params"], g["d_model"], g["H"], g["r_list"])
+    ids = g["ids"]
+    n0 = ids.shape[1] - 4
+    _, caches, states = m.forward(ids[:, :n0], return_state=True)
+    for t in range(n0, ids.shape[1]):
+        step, caches, states = m.forward_step(ids[:, t:t + 1], caches, states)
+        full = m.forward(ids[:, :t + 1], last_only=True)
+        torch.testing.assert_close(step, full, rtol=1e-9, atol=1e-9)
+
+
+LM_MUTATIONS = ["post_ln", "untied_head_transpose", "relu_mlp", "ln_eps_zero_mean"]
+
+
+@pytest.mark.parametrize("mutation", LM_MUTATIONS)
+def test_lm_planted_mistakes_are_caught(mutation, monkeypatch):
+    g = _lm_golden("2l_r16")
+    m = ref.SubwordLMRef(g["params"], g["d_model"], g["H"], g["r_list"])
+    if mutation == "post_ln":  # normalise after the residual add instead of before the sublayer
+        def fwd(ids):
+            x = m.emb[ids]
+            for attn, t in m.layers:
+                x = ref.layer_norm(x + attn.forward(x, eps=m.attn_eps), t["ln_1.weight"], t["ln_1.bias"])
+                x = ref.layer_norm(x + m._mlp(t, x), t["ln_2.weight"], t["ln_2.bias"])
+            return m._head(x)
+        out = fwd(g["ids"])
+    else:
+        if mutation == "untied_head_transpose":
+            monkeypatch.setattr(m, "_head", lambda x: ref.layer_norm(x, *m.lnf) @ m.emb[:, torch.randperm(
+                m.emb.shape[1], generator=torch.Generator().manual_seed(0))].T)
+        elif mutation == "relu_mlp":  # (erf vs tanh GELU differ by ~2e-5 here; nn.GELU pins the erf form)
+            monkeypatch.setattr(ref, "gelu", F.relu)
+        elif mutation == "ln_eps_zero_mean":  # RMS-style normalisation without the mean
+            monkeypatch.setattr(ref, "layer_norm",
+                                lambda x, w, b, eps=1e-5: x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w + b)
+        out = m.forward(g["ids"])
+    assert not torch.allclose(out.float(), g["logits"], rtol=1e-3, atol=1e-3), mutation
