@@ -3,28 +3,40 @@
 //
 // Replaces exact_attention_triton / _fwd_kernel (src/exact_attention.py:46-188).
 //
-// Block = 4 waves x 32 query rows (BM = 128), keys in tiles of BN = 64.
-// Per tile and wave:
-//   S^T[key, query] = K_tile Q^T            v_mfma_f32_32x32x16 (A = K from LDS, B = Q in registers;
+// Block = 4 waves x 32 query rows (BM = 128), keys in tiles of BN = 64,
+// consumed as two 32-key halves.  Per half and wave:
+//   S^T[key, query] = K_half Q^T            v_mfma_f32_32x32x16 (A = K from LDS, B = Q in registers;
 //                                           f32 inputs add the hi*lo and lo*hi bf16 products)
-//   online softmax in the base-2 domain     each lane owns one query row: its 32 scores of a
-//                                           tile sit in its registers and in lane l^32
-//   O^T[dv, query] += V_tile^T P^T          A = V^T from LDS (stored transposed), B = P straight
+//   P = exp2(c S - m)                       c = sm_scale log2 e; each lane owns one query row
+//                                           (its 16 scores of the half sit in its registers and
+//                                           in lane l^32), m = the row's reference max
+//   O^T[dv, query] += V_half^T P^T          A = V^T from LDS (stored transposed), B = P straight
 //                                           from the score registers (keys permuted consistently)
-//   l[query] += 1^T P^T                     the row sum on the matrix core (A = ones), over the
-//                                           same rounded P that enters O (f32 inputs: an exact f32
-//                                           sum of the unrounded P)
-// so the row max and the rescale of O never leave a lane pair.  The rescale
-// is lazy: the reference max moves only when a tile's max exceeds it by more
-// than kTau (log2 units), so P stays below 2^kTau and O is rarely rescaled.
+//   l[query] += sum P                       dot2 of the packed 16-bit P with (1, 1): the row sum
+//                                           of the same rounded P that enters O (f32 inputs: an
+//                                           exact f32 sum of the unrounded P)
+// The next half's QK^T does not depend on this half's exponentials, so the
+// matrix core and the VALU can overlap.  The reference max m is set by the
+// first half and moves only when a later logit exceeds it by more than kTau
+// (log2 units; P stays below 2^kTau), which rescales O and l.  A tile needs no
+// row max at all when the Cauchy-Schwarz bound c |q| |k| (the key norms are
+// taken while the tile is staged) is within m + kTau for every key of the tile
+// and every row of the wave.
 // K (row-major) and V^T tiles are double-buffered in LDS; the next tile's
 // range-checked buffer loads are in flight while the current tile is consumed.
+// V^T rows hold their 64 keys in operand order (each 16-byte group is the 8
+// keys one lane's operand takes) at a pitch of 36 dwords, and each half-wave
+// of the transposing stores covers the 32 key pairs of one 16-byte column:
+// both the stores and the 16-byte operand reads are free of bank conflicts.
+#include <type_traits>
+
 #include "hofa_mfma.h"
 
 namespace hofa {
 namespace {
 
 constexpr int BM = 128, BN = 64, NT = 256;
+constexpr int VTP = 36;  // V^T row pitch in dwords (64 keys + 8 pad bf16)
 
 struct AttnFwdK {
     const void *q, *k, *v, *mix;
@@ -41,29 +53,76 @@ struct AttnFwdK {
     float c;  // sm_scale * log2(e)
 };
 
+// acc + p.lo + p.hi for a dword of two 16-bit probabilities (v_dot2 with (1, 1)).
+template <int DT>
+__device__ __forceinline__ float dot2_ones(uint32_t p, float acc) {
+    if constexpr (kF16Ops<DT>)
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), __builtin_bit_cast(f16x2, 0x3C003C00u), acc, false);
+    else
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p), __builtin_bit_cast(bf16x2, 0x3F803F80u),
+                                               acc, false);
+}
+
+// x(l) + x(l ^ 32) and max(x(l), x(l ^ 32)) for every lane: one
+// v_permlane32_swap of x with itself puts both halves side by side (either
+// way round, so the sum / max is the same).
+__device__ __forceinline__ float xor32_sum(float x) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float xor32_max(float x) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
+// Sum over each group of N consecutive lanes (N = 1, 2, 4 within quads via
+// DPP; 8 adds one swizzle), without a round trip through LDS for N <= 4.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+    if constexpr (N >= 2) x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));
+    if constexpr (N >= 4) x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));
+    if constexpr (N >= 8) x += __shfl_xor(x, 4);
+    return x;
+}
+
+// Position of key `key` (0..63 within a tile) in its V^T row: bits 2 and 3 of
+// the key swap, so keys {4h..4h+3, 8+4h..8+4h+3} of each 16-key step (the
+// operand of the lanes with hi = h) form one 16-byte group.
+__device__ __forceinline__ int vt_pos(int key) { return (key & ~0xC) | ((key >> 1) & 4) | ((key << 1) & 8); }
+
 template <int DT, int R, int D>
 __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_kernel(AttnFwdK a) {
     using in_t = typename Stor<DT>::type;
     constexpr int KS = R / 16;       // MFMA k-steps of S^T
     constexpr int MB = D / 32;       // 32-row blocks of O^T
     constexpr int KP = R + 8;        // K tile pitch in LDS (elements)
-    constexpr int VP = BN + 4;       // V^T tile pitch in LDS (elements)
     constexpr int KCH = BN * R / 8;  // 16-byte K chunks per tile
     constexpr int NKC = (KCH + NT - 1) / NT;
-    constexpr int NVP = (BN / 2) * (D / 8) / NT;  // (2 keys x 8 dv) pieces of V per thread
-    static_assert(NVP >= 1 && (BN / 2) * (D / 8) % NT == 0, "V tile split");
-    constexpr bool SPLIT = DT == HOFA_F32;         // logits from split-bf16 operands
-    constexpr int KLO = SPLIT ? BN * KP : 0;      // offset of the K remainder tile
+    constexpr int CPR = D / 8;                  // 16-byte chunks per V row
+    constexpr int NVP = (BN / 2) * CPR / NT;    // (2 keys x 8 dv) pieces of V per thread
+    static_assert(NVP >= 1 && (BN / 2) * CPR % NT == 0, "V tile split");
+    constexpr bool SPLIT = DT == HOFA_F32;      // logits from split-bf16 operands
+    constexpr int KLO = SPLIT ? BN * KP : 0;    // offset of the K remainder tile
+    constexpr float kTau = kF16Ops<DT> ? 15.f : 64.f;  // P <= 2^kTau (f16 operands: below 65504)
     __shared__ __attribute__((aligned(16))) uint16_t sK[2][BN * KP + KLO];
-    __shared__ __attribute__((aligned(16))) uint16_t sV[2][D * VP];
+    __shared__ __attribute__((aligned(16))) uint32_t sV[2][D * VTP];
+    __shared__ float sKn[2][BN];  // squared norm of every key row of each tile
 
+    // Each block runs two row blocks of one head, qb = nq - 1 - j and then
+    // qb = j: every pair holds the same causal work, so all blocks finish
+    // together (one round of blocks, no tail of short ones).
     const int nq = (a.T + BM - 1) / BM;
-    int bh, qb;
-    xcd_remap(blockIdx.x, nq, a.B * a.H, &bh, &qb);
+    const int npair = (nq + 1) / 2;
+    int bh, pj;
+    xcd_remap(blockIdx.x, npair, a.B * a.H, &bh, &pj);
     const int b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hi = lane >> 5;  // which half of the wave
+    const int nrun = pj < nq - 1 - pj ? 2 : 1;
+#pragma nounroll
+    for (int run = 0; run < nrun; ++run) {  // the LDS tiles of the first were last read before its final barrier
+    const int qb = run == 0 ? nq - 1 - pj : pj;
     const int q0 = qb * BM;
     const int qw0 = q0 + 32 * w;  // first query row of this wave
     const int qrow = qw0 + (lane & 31);
@@ -72,165 +131,220 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
     const in_t *kp = (const in_t *)a.k + b * a.k_sb + h * a.k_sh;
     const in_t *vp = (const in_t *)a.v + b * a.v_sb + h * a.v_sh;
 
+    // B operand Q (f32 inputs: hi/lo); qn = c |q| with a relative 2^-10 margin
     u32x4 qop[KS], qlo[KS];
+    float qss = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         qop[ks] = qrow < a.T ? load_op8<DT>(qp + (int64_t)qrow * a.q_st + 16 * ks + 8 * hi) : u32x4{0, 0, 0, 0};
         if constexpr (SPLIT)
             qlo[ks] = qrow < a.T ? load_lo8_f32((const float *)qp + (int64_t)qrow * a.q_st + 16 * ks + 8 * hi)
                                  : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float x0 = op_to_f32<DT>(qop[ks][e] & 0xffffu), x1 = op_to_f32<DT>(qop[ks][e] >> 16);
+            if constexpr (SPLIT) {
+                x0 += op_to_f32<DT>(qlo[ks][e] & 0xffffu);
+                x1 += op_to_f32<DT>(qlo[ks][e] >> 16);
+            }
+            qss = fmaf(x0, x0, fmaf(x1, x1, qss));
+        }
     }
+    const float qn = __builtin_amdgcn_sqrtf(xor32_sum(qss)) * (a.c * (1.f + 1.f / 1024.f));
 
     const int kend = min(a.T, q0 + BM);
     const int ntiles = (kend + BN - 1) / BN;
 
     // ---- cooperative tile loader (global -> registers -> LDS): the next tile's
     // loads are in flight while the current tile is consumed
-    u32x4 kreg[1][NKC], klo[1][NKC];
-    u32x4 vreg[1][NVP][2];
+    u32x4 kreg[NKC], klo[NKC];
+    u32x4 vreg[NVP][2];
     constexpr int ES = sizeof(in_t);
     const __amdgpu_buffer_rsrc_t rk = rows_rsrc(kp, (uint32_t)(a.T * a.k_st * ES));
     const __amdgpu_buffer_rsrc_t rv = rows_rsrc(vp, (uint32_t)(a.T * a.v_st * ES));
-    auto gload = [&](int kt, int sl) {
+    // V piece pi: key pair kp = pi % 32 (rows 2kp, 2kp + 1) x 16-byte column cch = pi / 32
+    auto gload = [&](int kt) {
         const int k0 = kt * BN;
 #pragma unroll
         for (int i = 0; i < NKC; ++i) {
             const int ci = min(tid + NT * i, KCH - 1);  // threads past the tile reload its last chunk
             const int row = ci / (R / 8), part = ci % (R / 8);
             const uint32_t off = (uint32_t)(((k0 + row) * a.k_st + 8 * part) * ES);
-            kreg[sl][i] = bload_op8<DT>(rk, off, SPLIT ? &klo[sl][i] : nullptr);
+            kreg[i] = bload_op8<DT>(rk, off, SPLIT ? &klo[i] : nullptr);
         }
 #pragma unroll
         for (int i = 0; i < NVP; ++i) {
-            const int pi = tid + NT * i;
-            const int kpair = pi / (D / 8), cch = pi % (D / 8);
+            const int pi = tid + NT * i, kpair = pi % 32, cch = pi / 32;
             const uint32_t off = (uint32_t)(((k0 + 2 * kpair) * a.v_st + 8 * cch) * ES);
-            vreg[sl][i][0] = bload_op8<DT>(rv, off);
-            vreg[sl][i][1] = bload_op8<DT>(rv, off + (uint32_t)(a.v_st * ES));
+            vreg[i][0] = bload_op8<DT>(rv, off);
+            vreg[i][1] = bload_op8<DT>(rv, off + (uint32_t)(a.v_st * ES));
         }
     };
-    auto lstore = [&](int buf, int sl) {
+    auto lstore = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < NKC; ++i) {
             const int ci = tid + NT * i;
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float x0 = op_to_f32<DT>(kreg[i][e] & 0xffffu), x1 = op_to_f32<DT>(kreg[i][e] >> 16);
+                if constexpr (SPLIT) {
+                    x0 += op_to_f32<DT>(klo[i][e] & 0xffffu);
+                    x1 += op_to_f32<DT>(klo[i][e] >> 16);
+                }
+                ss = fmaf(x0, x0, fmaf(x1, x1, ss));
+            }
+            ss = group_sum<R / 8>(ss);  // the row's chunks sit in R/8 consecutive lanes
             if (ci < KCH) {
                 const int row = ci / (R / 8), part = ci % (R / 8);
-                *(u32x4 *)&sK[buf][row * KP + 8 * part] = kreg[sl][i];
-                if constexpr (SPLIT) *(u32x4 *)&sK[buf][KLO + row * KP + 8 * part] = klo[sl][i];
+                if (part == 0) sKn[buf][row] = ss;
+                *(u32x4 *)&sK[buf][row * KP + 8 * part] = kreg[i];
+                if constexpr (SPLIT) *(u32x4 *)&sK[buf][KLO + row * KP + 8 * part] = klo[i];
             }
         }
 #pragma unroll
         for (int i = 0; i < NVP; ++i) {
-            const int pi = tid + NT * i;
-            const int kpair = pi / (D / 8), cch = pi % (D / 8);
+            const int pi = tid + NT * i, kpair = pi % 32, cch = pi / 32;
+            uint32_t *dst = &sV[buf][8 * cch * VTP + (vt_pos(2 * kpair) >> 1)];
             // transpose a (2 keys x 8 dv) piece: dv row gets the key pair as one dword
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const uint32_t x0 = vreg[sl][i][0][e], x1 = vreg[sl][i][1][e];
-                *(uint32_t *)&sV[buf][(8 * cch + 2 * e) * VP + 2 * kpair] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
-                *(uint32_t *)&sV[buf][(8 * cch + 2 * e + 1) * VP + 2 * kpair] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+                const uint32_t x0 = vreg[i][0][e], x1 = vreg[i][1][e];
+                dst[(2 * e) * VTP] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+                dst[(2 * e + 1) * VTP] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
             }
         }
     };
 
-    constexpr float kTau = 8.f;
-    constexpr uint32_t kOne2 = kF16Ops<DT> ? 0x3C003C00u : 0x3F803F80u;  // two 16-bit 1.0
-    const u32x4 ones = {kOne2, kOne2, kOne2, kOne2};
     float mref = -INFINITY;  // reference max of the scaled logits (base 2)
-    f32x16 o[MB], lacc;
+    f32x16 o[MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[mb][v] = 0.f;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) lacc[v] = 0.f;
+    float lsum = 0.f;  // this lane's part of the row sum (the partner lane l^32 holds the rest)
 
-    float lsum = 0.f;  // f32 inputs: exact row sum of the unrounded probabilities
-    auto tile = [&](int kt, int buf) {
-        const int k0 = kt * BN;
-        if (k0 > qw0 + 31) return;  // every key of this tile is after this wave's queries
-        f32x16 s[2];
+    // One 32-key half (keys k0 .. k0+31, all at or before every query row of
+    // the wave unless MASK).  EXACT forms the row max and moves the reference
+    // (rescaling O and l) when a logit exceeds it by more than kTau; without
+    // EXACT the caller has shown with the Cauchy-Schwarz bound that no logit
+    // does, and the half runs without branches.
+    auto half = [&](int buf, int kb, int k0, auto exact, auto mask) {
+        f32x16 s = {};
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            s[kb] = f32x16{};
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const u32x4 ka = *(const u32x4 *)&sK[buf][(32 * kb + (lane & 31)) * KP + 16 * ks + 8 * hi];
-                s[kb] = mfma32<DT>(ka, qop[ks], s[kb]);
-                if constexpr (SPLIT) {
-                    const u32x4 kl = *(const u32x4 *)&sK[buf][KLO + (32 * kb + (lane & 31)) * KP + 16 * ks + 8 * hi];
-                    s[kb] = mfma32<DT>(ka, qlo[ks], s[kb]);
-                    s[kb] = mfma32<DT>(kl, qop[ks], s[kb]);
-                }
+        for (int ks = 0; ks < KS; ++ks) {
+            const u32x4 ka = *(const u32x4 *)&sK[buf][(32 * kb + (lane & 31)) * KP + 16 * ks + 8 * hi];
+            s = mfma32<DT>(ka, qop[ks], s);
+            if constexpr (SPLIT) {
+                const u32x4 kl = *(const u32x4 *)&sK[buf][KLO + (32 * kb + (lane & 31)) * KP + 16 * ks + 8 * hi];
+                s = mfma32<DT>(ka, qlo[ks], s);
+                s = mfma32<DT>(kl, qop[ks], s);
             }
         }
-        if (k0 + BN - 1 > qw0 || k0 + BN > a.T) {  // tile crosses the diagonal or the end
-            const int lim = min(qrow, a.T - 1) - k0 - 4 * hi;  // visible iff row offset <= lim
+        if constexpr (decltype(mask)::value) {  // causal mask (keys past T are past every valid row)
+            const int lim = qrow - k0 - 4 * hi;  // visible iff row offset <= lim
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int v = 0; v < 16; ++v)
-                    s[kb][v] = 32 * kb + 8 * (v / 4) + (v % 4) <= lim ? s[kb][v] : -INFINITY;
+            for (int v = 0; v < 16; ++v) s[v] = 8 * (v / 4) + (v % 4) <= lim ? s[v] : -INFINITY;
         }
-        float t8[8];  // max as a tree (short dependency chains)
+        if constexpr (decltype(exact)::value) {
+            float t4[4];  // the max as a tree (short dependency chains)
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            t8[i] = fmaxf(fmaxf(s[0][i], s[0][i + 8]), fmaxf(s[1][i], s[1][i + 8]));
+            for (int i = 0; i < 4; ++i) t4[i] = fmaxf(fmaxf(s[i], s[i + 4]), fmaxf(s[i + 8], s[i + 12]));
+            float mx = fmaxf(fmaxf(t4[0], t4[1]), fmaxf(t4[2], t4[3]));
+            mx = xor32_max(mx) * a.c;  // every row sees at least one key of the half
+            if (__ballot(mx > mref + kTau)) {  // (re)set the reference: rescale O and l
+                const float mn = mx > mref + kTau ? mx : mref;
+                const float alpha = fast_exp2(mref - mn);  // 0 while O and l are still empty
 #pragma unroll
-        for (int i = 0; i < 4; ++i) t8[i] = fmaxf(t8[i], t8[i + 4]);
-        float mx = fmaxf(fmaxf(t8[0], t8[1]), fmaxf(t8[2], t8[3]));
-        mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.c;
-        if (__ballot(mx > mref + kTau)) {  // some row's max moved far: rescale (wave-uniform branch)
-            const float mn = fmaxf(mref, mx);
-            const float alpha = fast_exp2(mref - mn);  // 0 on the first tile (mref = -inf)
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb) o[mb] *= alpha;
-            if constexpr (SPLIT) lsum *= alpha;
-            else lacc *= alpha;
-            mref = mn;
+                for (int mb = 0; mb < MB; ++mb) o[mb] *= alpha;
+                lsum *= alpha;
+                mref = mn;
+            }
         }
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) s[kb][v] = fast_exp2(fmaf(s[kb][v], a.c, -mref));
+        for (int v = 0; v < 16; ++v) s[v] = fast_exp2(fmaf(s[v], a.c, -mref));
         if constexpr (SPLIT) {
             float ps[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) ps[v % 4] += s[kb][v];
+            for (int v = 0; v < 16; ++v) ps[v % 4] += s[v];
             lsum += (ps[0] + ps[1]) + (ps[2] + ps[3]);
         }
 #pragma unroll
-        for (int ks4 = 0; ks4 < 4; ++ks4) {
-            const u32x4 pb = pack8<DT>(s[ks4 / 2], 8 * (ks4 % 2));
-            if constexpr (!SPLIT) lacc = mfma32<DT>(ones, pb, lacc);
+        for (int k2 = 0; k2 < 2; ++k2) {
+            const int ks4 = 2 * kb + k2;
+            const u32x4 pb = pack8<DT>(s, 8 * k2);
+            if constexpr (!SPLIT) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) lsum = dot2_ones<DT>(pb[e], lsum);
+            }
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
-                const uint16_t *vr = &sV[buf][(32 * mb + (lane & 31)) * VP + 16 * ks4 + 4 * hi];
-                const uint2 lo = *(const uint2 *)vr, hi8 = *(const uint2 *)(vr + 8);
-                const u32x4 va = {lo.x, lo.y, hi8.x, hi8.y};
+                const u32x4 va = *(const u32x4 *)&sV[buf][(32 * mb + (lane & 31)) * VTP + 4 * (2 * ks4 + hi)];
                 o[mb] = mfma32<DT>(va, pb, o[mb]);
             }
         }
     };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
 
-    // tile kt lives in LDS buffer kt%2
-    gload(0, 0);
-    lstore(0, 0);
+    // Tiles [0, nfull) lie at or before the first query row of the block, so
+    // every key is visible to every row; the last one or two tiles hold the
+    // diagonal.  Each loop iteration has one barrier, whichever loop a wave is
+    // in, so the waves of the block stay in step through the tile staging.
+    const int nfull = min(q0 / BN, ntiles);
+    gload(0);
+    lstore(0);
     __syncthreads();
-    for (int kt = 0; kt < ntiles; ++kt) {
+    // The fast run needs no row max while every key k of the tile and every row
+    // q of the wave satisfy c |q| |k| + 2^-6 <= m_q + kTau, i.e. while
+    // |k|^2 <= theta2 = (min over rows of (m_q + kTau - 2^-6) / (c |q|))^2;
+    // theta2 changes only when a reference moves (after an exact tile).
+    float theta2 = -1.f;  // no reference yet: the first tile is exact
+    auto update_theta = [&]() {
+        float t = qn > 0.f ? (mref + kTau - 1.f / 64.f) / qn : INFINITY;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) t = fminf(t, __shfl_xor(t, off));
+        theta2 = t >= 0.f ? t * t : -1.f;
+    };
+    int kt = 0;
+    while (kt < nfull) {
+        for (; kt < nfull; ++kt) {  // fast run
+            if (__ballot(sKn[kt & 1][lane] > theta2)) break;  // lane = key row of the tile; wave-uniform
+            const bool more = kt + 1 < ntiles;
+            if (more) gload(kt + 1);
+            half(kt & 1, 0, kt * BN, F_{}, F_{});
+            half(kt & 1, 1, kt * BN + 32, F_{}, F_{});
+            if (more) lstore((kt + 1) & 1);
+            __syncthreads();
+        }
+        if (kt == nfull) break;
+        // one tile with the exact row max (sets or moves the reference)
         const bool more = kt + 1 < ntiles;
-        if (more) gload(kt + 1, 0);
-        tile(kt, kt & 1);
-        if (more) lstore((kt + 1) & 1, 0);
+        if (more) gload(kt + 1);
+        half(kt & 1, 0, kt * BN, T_{}, F_{});
+        half(kt & 1, 1, kt * BN + 32, T_{}, F_{});
+        if (more) lstore((kt + 1) & 1);
+        __syncthreads();
+        update_theta();
+        ++kt;
+    }
+    // the diagonal tiles: per half, fully visible (k0 < qw0), diagonal (k0 == qw0) or past the wave
+    for (; kt < ntiles; ++kt) {
+        const bool more = kt + 1 < ntiles;
+        if (more) gload(kt + 1);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int k0 = kt * BN + 32 * kb;
+            if (k0 < qw0) half(kt & 1, kb, k0, T_{}, F_{});
+            else if (k0 == qw0) half(kt & 1, kb, k0, T_{}, T_{});
+        }
+        if (more) lstore((kt + 1) & 1);
         __syncthreads();
     }
 
     // ---- epilogue: y (+)= mix * O, optional O and lse
-    // every row of the ones-product holds the query's sum; f32 inputs sum in f32
-    const float l = SPLIT ? lsum + __shfl_xor(lsum, 32) : lacc[0];
-    if (qrow >= a.T) return;
+    const float l = xor32_sum(lsum);
+    if (qrow >= a.T) continue;
     const float inv = 1.f / l;
     const float mixv = a.mix ? load_any(a.mix, a.mix_dt, b * a.m_sb + h * a.m_sh + (int64_t)qrow * a.m_st) : 1.f;
     in_t *yr = (in_t *)a.y + b * a.y_sb + h * a.y_sh + (int64_t)qrow * a.y_st;
@@ -273,12 +387,13 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
             }
         }
     if (a.lse && hi == 0) a.lse[(int64_t)bh * a.T + qrow] = mref + __log2f(l);
+    }
 }
 
 template <int DT, int R, int D>
 void launch(const AttnFwdK &k, hipStream_t s) {
     const int nq = (k.T + BM - 1) / BM;
-    hipLaunchKernelGGL((attn_fwd_kernel<DT, R, D>), dim3(nq * k.B * k.H), dim3(NT), 0, s, k);
+    hipLaunchKernelGGL((attn_fwd_kernel<DT, R, D>), dim3((nq + 1) / 2 * k.B * k.H), dim3(NT), 0, s, k);
 }
 
 template <int DT>
