@@ -4,22 +4,34 @@
 // No reference counterpart in the repository's own code: the reference
 // trains through autograd of torch SDPA (src/HybridOutlierFactorizedAttentionTrain.py:258-259).
 //
-// With P = exp2(S * c - lse2) (c = sm_scale * log2(e)), dP = dO V^T,
-// dS = P (.) (dP - Dt), Dt = rowsum(dO (.) O):
+// With P = exp2(c S - lse) (c = sm_scale * log2(e), lse base 2),
+// dP = dO V^T, dS = P (.) (dP - Dt), Dt = rowsum(dO (.) O):
 //   dV = P^T dO,  dK = sm_scale dS^T Q,  dQ = sm_scale dS K.
 // Two kernels, no atomics:
 //   attn_bwd_dkdv_kernel  block = 128 keys (4 waves x 32, lane = key), loop over
-//                         the query tiles at or after the block; S, dP in the
-//                         C[query, key] layout, so P and dS feed the dV^T and
-//                         dK^T products straight from registers (A = dO^T, Q^T
-//                         from LDS).
+//                         the 64-query tiles at or after the block; S and dP in
+//                         the C[query, key] layout, so P and dS feed the dV^T and
+//                         dK^T products straight from registers as B operands.
 //   attn_bwd_dq_kernel    block = 128 queries (4 waves x 32, lane = query), loop
-//                         over the key tiles up to the diagonal; S^T, dP^T in the
-//                         C[key, query] layout, dQ^T = K^T dS^T.
+//                         over the 64-key tiles up to the diagonal; S^T, dP^T in
+//                         the C[key, query] layout, dQ^T = K^T dS^T.
+// The key (dK/dV kernel) or query (dQ kernel) operand of the logits carries
+// c as a 16-bit hi/lo pair, and the per-query terms -lse and -Dt enter the S
+// and dP products as one extra k-step (a hi/lo pair times ones), so the
+// accumulators come out of the matrix cores as c S - lse and dP - Dt and the
+// softmax needs one exp2 and one multiply per score.
+// Q/dO (dK/dV kernel) and K/V (dQ kernel) tiles are staged in LDS row-major
+// only; the operands that run along the tile's rows (dO^T, Q^T, K^T) are read
+// with gfx950's transposing LDS load ds_read_b64_tr_b16.  Tile rows are
+// swizzled in 16-byte granules so the row reads, the transposing reads and the
+// staging stores are free of bank conflicts.
 // Matrix operands are 16-bit (bf16 for bf16/f32 inputs, f16 for f16) with f32
 // accumulation, as in flash-attention backward passes; f32 inputs form the
 // logits from hi/lo operand pairs so the recomputed probabilities agree with
 // the forward's log-sum-exp.
+#include <cmath>
+#include <type_traits>
+
 #include "hofa_mfma.h"
 
 namespace hofa {
@@ -43,91 +55,211 @@ struct AttnBwdK {
     float sm_scale;
 };
 
-// Rows [t0, t0+64) of a [T, W] operand matrix, staged global -> registers
-// (fetch, issued a tile ahead) -> LDS (put): row-major ([64][W + pad]) and/or
-// transposed ([W][64 + pad]) 16-bit operands, rows past T zero; f32 inputs
-// also keep their bf16 rounding remainders (row-major).  256 threads, each
-// owning (2 rows x 8 columns) pieces.
+// A 64-row tile of width W (16-bit elements) in LDS: row pitch and the 16-byte
+// granule swizzle (granule g of row r lives at g ^ swz(r)).  W = 16 rows are
+// padded to 24 elements instead.  With 64 four-byte banks, 16-lane row reads
+// of one granule column, the 8-row x 64-byte footprint of a transposing read
+// and row-wise staging stores all touch distinct banks.
+template <int W>
+struct TileL {
+    static constexpr int PITCH = W == 16 ? 24 : W;
+    static constexpr int ELEMS = 64 * PITCH;
+    __device__ static constexpr int swz(int r) {
+        if constexpr (W == 16) return 0;
+        else if constexpr (W == 32) return (r >> 2) & 3;
+        else if constexpr (W == 64) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+        else return ((r & 3) << 2) | ((r >> 2) & 3);
+    }
+    // element offset of (row r, column c); c keeps its place inside its granule
+    __device__ static int off(int r, int c) { return r * PITCH + ((((c >> 3) ^ swz(r))) << 3) + (c & 7); }
+};
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint2 lds_tr16(const uint16_t *p) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)p);
+    return __builtin_bit_cast(uint2, v);
+}
+
+// A operand of v_mfma_f32_32x32x16 whose row index i runs along tile columns
+// [col0, col0 + 32) and whose k index runs along tile rows:
+//   lane l = 16 g + s, i = l % 32, k = 8 (l / 32) + e  <->  tile row krow0 + 8 (e / 4) + 4 (l / 32) + e % 4,
+// the order in which a C-layout accumulator's entries [8 k2, 8 k2 + 8) pack into
+// an operand (pack8).  ds_read_b64_tr_b16 hands output lane 4a + b of each
+// 16-lane group element b of the 8-byte reads of lanes a, a + 4, a + 8, a + 12,
+// so source lane s reads tile row krow0 + 4 (l / 32) + s / 4 at column
+// col0 + i0 + 4 (s % 4).  Tiles narrower than 32 columns (W = 16) fill rows
+// 16..31 of the operand with a copy of rows 0..15.
+template <int W>
+__device__ __forceinline__ u32x4 tr_operand(const uint16_t *tile, int krow0, int col0, int lane) {
+    const int g = lane >> 4, s = lane & 15;
+    const int i0 = W >= 32 ? 16 * (g & 1) : 0;
+    const int row = krow0 + 4 * (g >> 1) + (s >> 2);
+    const int col = col0 + i0 + 4 * (s & 3);
+    const uint2 a = lds_tr16(tile + TileL<W>::off(row, col));
+    const uint2 b = lds_tr16(tile + TileL<W>::off(row + 8, col));
+    return u32x4{a.x, a.y, b.x, b.y};
+}
+
+// Rows [t0, t0+64) of a [T, W] input matrix, staged global -> registers
+// (fetch, issued a tile ahead) -> LDS (put) as row-major 16-bit operands in the
+// TileL<W> layout, rows past T zero; f32 inputs also keep their bf16 rounding
+// remainders (same layout, second array).  256 threads, one 16-byte granule
+// (8 elements) of one row each per piece.
 template <int DT, int W>
-struct RowStage {
+struct TileStage {
     using in_t = typename Stor<DT>::type;
-    static constexpr int NPIECE = 32 * (W / 8);
+    static constexpr int NG = W / 8;
+    static constexpr int NPIECE = 64 * NG;
     static constexpr int NP = (NPIECE + NT - 1) / NT;
     static constexpr bool LO = DT == HOFA_F32;
-    u32x4 x0[NP], x1[NP], l0[LO ? NP : 1], l1[LO ? NP : 1];
+    u32x4 x[NP], l[LO ? NP : 1];
 
     __device__ void fetch(const in_t *base, int64_t st, int t0, int T) {
         const __amdgpu_buffer_rsrc_t r = rows_rsrc(base, (uint32_t)(T * st * sizeof(in_t)));
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
             const int pi = min((int)threadIdx.x + NT * i, NPIECE - 1);  // extra threads repeat the last piece
-            const int rp = pi / (W / 8), cc = pi % (W / 8);
-            const uint32_t off = (uint32_t)(((t0 + 2 * rp) * st + 8 * cc) * sizeof(in_t));
-            const uint32_t off1 = off + (uint32_t)(st * sizeof(in_t));
-            if constexpr (LO) {
-                x0[i] = bload_op8<DT>(r, off, &l0[i]);
-                x1[i] = bload_op8<DT>(r, off1, &l1[i]);
-            } else {
-                x0[i] = bload16(r, off);
-                x1[i] = bload16(r, off1);
-            }
+            const uint32_t off = (uint32_t)(((t0 + pi / NG) * st + 8 * (pi % NG)) * sizeof(in_t));
+            if constexpr (LO) x[i] = bload_op8<DT>(r, off, &l[i]);
+            else x[i] = bload16(r, off);
         }
     }
-    template <int PR, int PT, bool ROW, bool TR>
-    __device__ void put(uint16_t *row, uint16_t *tr, uint16_t *lo) const {
+    __device__ void put(uint16_t *tile, uint16_t *lo) const {
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
             const int pi = threadIdx.x + NT * i;
-            if (pi >= NPIECE) continue;
-            const int rp = pi / (W / 8), cc = pi % (W / 8);
-            const int r0 = 2 * rp;
-            if constexpr (ROW) {
-                *(u32x4 *)&row[r0 * PR + 8 * cc] = x0[i];
-                *(u32x4 *)&row[(r0 + 1) * PR + 8 * cc] = x1[i];
-            }
-            if constexpr (LO && ROW) {
-                *(u32x4 *)&lo[r0 * PR + 8 * cc] = l0[i];
-                *(u32x4 *)&lo[(r0 + 1) * PR + 8 * cc] = l1[i];
-            }
-            if constexpr (TR) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    *(uint32_t *)&tr[(8 * cc + 2 * e) * PT + r0] = __builtin_amdgcn_perm(x1[i][e], x0[i][e], 0x05040100u);
-                    *(uint32_t *)&tr[(8 * cc + 2 * e + 1) * PT + r0] = __builtin_amdgcn_perm(x1[i][e], x0[i][e], 0x07060302u);
-                }
-            }
+            if (NPIECE % NT != 0 && pi >= NPIECE) continue;
+            const int o = TileL<W>::off(pi / NG, 8 * (pi % NG));
+            *(u32x4 *)&tile[o] = x[i];
+            if constexpr (LO) *(u32x4 *)&lo[o] = l[i];
         }
     }
 };
 
-// A operand of a k-step of 16 along the permuted index of a C-layout tile:
-// lane reads entries [16ks + 4hi .. +3] and [16ks + 8 + 4hi .. +3] of its row.
-__device__ __forceinline__ u32x4 perm_a(const uint16_t *row, int ks, int hi) {
-    const uint16_t *p = row + 16 * ks + 4 * hi;
-    const uint2 lo = *(const uint2 *)p, h8 = *(const uint2 *)(p + 8);
-    return u32x4{lo.x, lo.y, h8.x, h8.y};
+// The same tile staged by the DMA path of 16-bit inputs: buffer loads that
+// write LDS directly (buffer_load_dwordx4 ... lds), each wave load filling
+// 1 KB of the tile image, lane j the 16-byte granule at 16 j.  A lane fetches
+// the source granule that the TileL<W> swizzle puts at its position; padding
+// granules (W = 16) and rows past T read out of range and land as zeros.
+// The loads count against vmcnt: the issuing wave waits for them before the
+// barrier that hands the buffer to the block.
+template <int W>
+struct TileDma {
+    static constexpr int GPR = TileL<W>::PITCH / 8;  // 16-byte granules per LDS row, padding included
+    static constexpr int NLOAD = GPR;                 // 64 rows x GPR granules / 64 lanes
+    template <class in_t>
+    __device__ static void fetch(uint16_t *tile, const in_t *base, int64_t st, int t0, int T, int wave, int lane) {
+        const __amdgpu_buffer_rsrc_t r = rows_rsrc(base, (uint32_t)(T * st * sizeof(in_t)));
+#pragma unroll
+        for (int i0 = 0; i0 < NLOAD; i0 += 4) {
+            const int i = i0 + wave;
+            if (NLOAD % 4 != 0 && i >= NLOAD) break;
+            const int p = 64 * i + lane;
+            const int row = p / GPR, pg = p % GPR;
+            const uint32_t off = pg >= W / 8
+                                     ? 0x80000000u
+                                     : (uint32_t)(((t0 + row) * st + 8 * (pg ^ TileL<W>::swz(row))) * sizeof(in_t));
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(tile + 512 * i), 16,
+                                                     off, 0, 0, 0);
+        }
+    }
+};
+
+// Wait for this wave's outstanding vector-memory loads (the LDS DMA of a tile).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// Operand dword of two 16-bit values (hi, lo) with hi + lo = x to about twice
+// the operand precision.
+template <int DT>
+__device__ __forceinline__ uint32_t split_pair(float x) {
+    const uint32_t h = pack2<DT>(x, 0.f) & 0xffffu;
+    const float r = x - op_to_f32<DT>(h);
+    return h | (pack2<DT>(r, 0.f) << 16);
 }
 
-template <int DT, int R, int D>
-// Three waves per SIMD for the 16-bit d_h=64 kernels (LDS allows three blocks per CU).
-__global__ __launch_bounds__(NT, (DT != HOFA_F32 && D == 64 && R <= 32) ? 3 : 1) void attn_bwd_dkdv_kernel(AttnBwdK a) {
+// 8 consecutive input elements times `scale` (in f32) as a 16-bit operand
+// pair hi + lo (about twice the operand precision), zeros when !valid.
+template <int DT>
+__device__ __forceinline__ void load_scaled_op8(const typename Stor<DT>::type *p, float scale, bool valid, u32x4 &hi,
+                                                u32x4 &lo) {
+    float x[8];
+    if (valid) {
+        const u32x4 w0 = *(const u32x4 *)p;
+        if constexpr (DT == HOFA_F32) {
+            const u32x4 w1 = *(const u32x4 *)(p + 4);
+            unpack16<DT>(w0, x);
+            unpack16<DT>(w1, x + 4);
+        } else {
+            unpack16<DT>(w0, x);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] *= scale;
+    split8<DT>(x, hi, lo);
+}
+
+// (1, 1) as a dword of 16-bit operands.
+template <int DT>
+constexpr uint32_t kOnes2 = kF16Ops<DT> ? 0x3C003C00u : 0x3F803F80u;
+
+// Scheduling hint for the row-operand products: the LDS reads of the block
+// issue as one group ahead of its matrix products, so their latencies overlap
+// instead of each read being waited for just before its product.
+// The logits' products (NS of them) go first so the exp2 of the softmax can
+// overlap the dP products that follow.
+template <int NS, int NP>
+__device__ __forceinline__ void sched_reads_then_mfma() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // DS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, NS, 0);  // MFMA: S
+    __builtin_amdgcn_sched_group_barrier(0x008, NP, 0);  // MFMA: dP
+}
+
+// Four consecutive elements of a gradient row (8-byte aligned for 16-bit
+// types, 16-byte for f32): one vector load / store, rounding on store.
+template <int DT>
+struct Run4 {
     using in_t = typename Stor<DT>::type;
+    using raw_t = typename std::conditional<DT == HOFA_F32, f32x4, uint2>::type;
+    raw_t r;
+    __device__ static Run4 load(const in_t *p) { return Run4{*(const raw_t *)p}; }
+    __device__ float get(int e) const {
+        if constexpr (DT == HOFA_F32) return r[e];
+        else return to_f32<DT>((uint16_t)((e < 2 ? r.x : r.y) >> (16 * (e & 1))));
+    }
+    __device__ static void store(in_t *p, const float *x) {
+        if constexpr (DT == HOFA_F32) {
+            *(f32x4 *)p = f32x4{x[0], x[1], x[2], x[3]};
+        } else {
+            *(uint2 *)p = uint2{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3])};
+        }
+    }
+};
+
+template <int DT, int R, int D>
+constexpr int dkdv_occupancy() { return (DT != HOFA_F32 && D == 64 && R <= 32) ? 3 : 1; }
+template <int DT, int R, int D>
+constexpr int dq_occupancy() { return (DT != HOFA_F32 && D == 64 && R <= 32) ? 4 : 1; }
+
+template <int DT, int R, int D>
+__global__ __launch_bounds__(NT, (dkdv_occupancy<DT, R, D>())) void attn_bwd_dkdv_kernel(AttnBwdK a) {
+    using in_t = typename Stor<DT>::type;
+    using LQ = TileL<R>;
+    using LO = TileL<D>;
     constexpr int KS = R / 16, DKS = D / 16, MB = D / 32;
     constexpr int RB = (R + 31) / 32;  // 32-row blocks of dK^T
-    constexpr int PQ = R + 8, PO = D + 8, PT = BQ + 4;
     constexpr bool SPL = DT == HOFA_F32;
-    __shared__ __attribute__((aligned(16))) uint16_t sQ[2][BQ * PQ];
-    __shared__ __attribute__((aligned(16))) uint16_t sQlo[2][SPL ? BQ * PQ : 8];
-    __shared__ __attribute__((aligned(16))) uint16_t sQt[2][RB * 32 * PT];
-    __shared__ __attribute__((aligned(16))) uint16_t sO[2][BQ * PO];
-    __shared__ __attribute__((aligned(16))) uint16_t sOt[2][D * PT];
-    __shared__ __attribute__((aligned(16))) float sL[2][BQ];
-    __shared__ __attribute__((aligned(16))) float sD[2][BQ];
+    __shared__ __attribute__((aligned(16))) uint16_t sQ[2][LQ::ELEMS];
+    __shared__ __attribute__((aligned(16))) uint16_t sQlo[2][SPL ? LQ::ELEMS : 8];
+    __shared__ __attribute__((aligned(16))) uint16_t sO[2][LO::ELEMS];
+    __shared__ __attribute__((aligned(16))) uint32_t sX[2][2][BQ];  // per query: (-lse/c, -Dt) as hi/lo pairs
 
     const int nkb = (a.T + BKB - 1) / BKB;
     int bh, kblk;
-    xcd_remap(blockIdx.x, nkb, a.B * a.H, &bh, &kblk);
-    kblk = nkb - 1 - kblk;  // xcd_remap walks row blocks last-first; key blocks near 0 have the most work
+    xcd_rank_remap(blockIdx.x, nkb, a.B * a.H, &bh, &kblk);  // key blocks near 0 have the most work
     const int b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x, lane = tid & 63, hi = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -142,20 +274,17 @@ __global__ __launch_bounds__(NT, (DT != HOFA_F32 && D == 64 && R <= 32) ? 3 : 1)
     const float *lse = a.lse + (int64_t)bh * a.T;
     const float *dtp = a.dt + (int64_t)bh * a.T;
 
-    // B operands: K (k = dims) and V (k = dv) of this lane's key
-    u32x4 kop[KS], klo[KS], vop[DKS];
+    // B operands: c K as a hi/lo pair (k = dims), so the logits come out of the
+    // matrix cores in base-2 units, V (k = dv) of this lane's key, and ones
+    // for the shift k-step
+    u32x4 kh[KS], kl[KS], vop[DKS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        kop[ks] = key < a.T ? load_op8<DT>(kp + (int64_t)key * a.k_st + 16 * ks + 8 * hi) : u32x4{0, 0, 0, 0};
-        if constexpr (SPL)
-            klo[ks] = key < a.T ? load_lo8_f32((const float *)kp + (int64_t)key * a.k_st + 16 * ks + 8 * hi)
-                                : u32x4{0, 0, 0, 0};
-    }
+    for (int ks = 0; ks < KS; ++ks)
+        load_scaled_op8<DT>(kp + (int64_t)key * a.k_st + 16 * ks + 8 * hi, a.c, key < a.T, kh[ks], kl[ks]);
 #pragma unroll
     for (int ks = 0; ks < DKS; ++ks)
         vop[ks] = key < a.T ? load_op8<DT>(vp + (int64_t)key * a.v_st + 16 * ks + 8 * hi) : u32x4{0, 0, 0, 0};
-    // rows R..32*RB-1 of Q^T stay zero
-    for (int i = tid; i < 2 * RB * 32 * PT; i += NT) (&sQt[0][0])[i] = 0;
+    const u32x4 ones = {hi ? 0u : kOnes2<DT>, 0u, 0u, 0u};
 
     f32x16 dvt[MB], dkt[RB];
 #pragma unroll
@@ -167,123 +296,170 @@ __global__ __launch_bounds__(NT, (DT != HOFA_F32 && D == 64 && R <= 32) ? 3 : 1)
 #pragma unroll
         for (int v = 0; v < 16; ++v) dkt[rb][v] = 0.f;
 
-    RowStage<DT, R> stq;
-    RowStage<DT, D> sto;
+    TileStage<DT, R> stq;
+    TileStage<DT, D> sto;
+    // per-query lse / Dt of the staged tile: raw loads at fetch (no wait on
+    // the tile's loads in flight), shifted hi/lo pairs formed at put
     float ls = 0.f, ds = 0.f;
-    auto fetch = [&](int q0) {
-        stq.fetch(qp, a.q_st, q0, a.T);
-        sto.fetch(op, a.o_st, q0, a.T);
+    auto fetch = [&](int buf, int q0) {
+        if constexpr (SPL) {
+            stq.fetch(qp, a.q_st, q0, a.T);
+            sto.fetch(op, a.o_st, q0, a.T);
+        } else {
+            TileDma<R>::fetch(sQ[buf], qp, a.q_st, q0, a.T, w, lane);
+            TileDma<D>::fetch(sO[buf], op, a.o_st, q0, a.T, w, lane);
+        }
         if (tid < BQ) {
-            ls = q0 + tid < a.T ? lse[q0 + tid] : 0.f;
-            ds = q0 + tid < a.T ? dtp[q0 + tid] : 0.f;
+            const int qi = min(q0 + tid, a.T - 1);
+            ls = lse[qi];
+            ds = dtp[qi];
         }
     };
-    auto put = [&](int buf) {
-        stq.template put<PQ, PT, true, true>(sQ[buf], sQt[buf], sQlo[buf]);
-        sto.template put<PO, PT, true, true>(sO[buf], sOt[buf], nullptr);
+    auto put = [&](int buf, int q0) {
+        if constexpr (SPL) {
+            stq.put(sQ[buf], sQlo[buf]);
+            sto.put(sO[buf], nullptr);
+        } else {
+            wait_vmem();
+        }
         if (tid < BQ) {
-            sL[buf][tid] = ls;
-            sD[buf][tid] = ds;
+            const bool in = q0 + tid < a.T;
+            sX[buf][0][tid] = split_pair<DT>(in ? -ls : 0.f);
+            sX[buf][1][tid] = split_pair<DT>(in ? -ds : 0.f);
         }
     };
-    fetch(k0);
-    __syncthreads();  // pad rows of Q^T cleared
-    put(0);
-    __syncthreads();
-    int buf = 0;
-    for (int q0 = k0; q0 < a.T; q0 += BQ, buf ^= 1) {
+    // One 64-query tile from LDS buffer buf.
+    auto tile = [&](int buf, int q0) {
         const bool more = q0 + BQ < a.T;
-        if (more) fetch(q0 + BQ);
-        if (q0 + BQ - 1 >= kw0) {  // some query of the tile sees this wave's keys
+        if (more) fetch(buf ^ 1, q0 + BQ);
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                f32x16 s = {}, dp = {};
-                const uint16_t *qrow = &sQ[buf][(32 * qb + (lane & 31)) * PQ];
+        for (int qb = 0; qb < 2; ++qb) {
+            const int qq0 = q0 + 32 * qb;
+            if (qq0 + 31 < kw0) continue;  // every query of the block precedes this wave's keys
+            const int rq = 32 * qb + (lane & 31);
+            // this block's query rows: every row operand read is issued before the products
+            u32x4 qa[KS], qla[SPL ? KS : 1], oa[DKS];
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    const u32x4 qa = *(const u32x4 *)(qrow + 16 * ks + 8 * hi);
-                    s = mfma32<DT>(qa, kop[ks], s);
-                    if constexpr (SPL) {
-                        s = mfma32<DT>(qa, klo[ks], s);
-                        s = mfma32<DT>(*(const u32x4 *)(&sQlo[buf][(32 * qb + (lane & 31)) * PQ] + 16 * ks + 8 * hi),
-                                       kop[ks], s);
-                    }
-                }
-                const uint16_t *orow = &sO[buf][(32 * qb + (lane & 31)) * PO];
+            for (int ks = 0; ks < KS; ++ks) {
+                qa[ks] = *(const u32x4 *)&sQ[buf][LQ::off(rq, 16 * ks + 8 * hi)];
+                if constexpr (SPL) qla[ks] = *(const u32x4 *)&sQlo[buf][LQ::off(rq, 16 * ks + 8 * hi)];
+            }
 #pragma unroll
-                for (int ks = 0; ks < DKS; ++ks) dp = mfma32<DT>(*(const u32x4 *)(orow + 16 * ks + 8 * hi), vop[ks], dp);
-                // P and dS in place (C[query, key]: lane = key, v -> query)
-                const bool edge = q0 + 32 * qb < kw0 + 31 || q0 + 32 * qb + 31 >= a.T || kw0 + 31 >= a.T;
-                // query offsets 8g + e of this lane (g = v/4, e = v%4) are visible iff vlo <= 8g + e <= vhi
-                const int vlo = key - q0 - 32 * qb - 4 * hi;
-                const int vhi = key < a.T ? a.T - 1 - q0 - 32 * qb - 4 * hi : -1;
+            for (int ks = 0; ks < DKS; ++ks) oa[ks] = *(const u32x4 *)&sO[buf][LO::off(rq, 16 * ks + 8 * hi)];
+            const uint32_t x2 = sX[buf][0][rq], y2 = sX[buf][1][rq];
+            const u32x4 xa = {hi ? 0u : x2, 0u, 0u, 0u};
+            const u32x4 ya = {hi ? 0u : y2, 0u, 0u, 0u};
+            // S' = c Q K^T - lse and dP' = dO V^T - Dt in C[query, key]
+            f32x16 s = {}, dp = {};
+            sched_reads_then_mfma<KS * (SPL ? 3 : 2) + 1, DKS + 1>();
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const f32x4 lq = *(const f32x4 *)&sL[buf][32 * qb + 8 * g + 4 * hi];
-                    const f32x4 dq = *(const f32x4 *)&sD[buf][32 * qb + 8 * g + 4 * hi];
+            for (int ks = 0; ks < KS; ++ks) {
+                s = mfma32<DT>(qa[ks], kh[ks], s);
+                s = mfma32<DT>(qa[ks], kl[ks], s);
+                if constexpr (SPL) s = mfma32<DT>(qla[ks], kh[ks], s);
+            }
+            s = mfma32<DT>(xa, ones, s);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int v = 4 * g + e;
-                        float p = fast_exp2(fmaf(s[v], a.c, -lq[e]));
-                        if (edge) p = (8 * g + e >= vlo && 8 * g + e <= vhi) ? p : 0.f;
-                        s[v] = p;
-                        dp[v] = p * (dp[v] - dq[e]);
-                    }
-                }
+            for (int ks = 0; ks < DKS; ++ks) dp = mfma32<DT>(oa[ks], vop[ks], dp);
+            dp = mfma32<DT>(ya, ones, dp);
+            // P and dS in place (lane = key, v -> query 8(v/4) + 4hi + v%4 of the block).
+            // Blocks on the diagonal or past T mask their logits to -inf first
+            // (query offset qo is visible iff vlo <= qo <= vhi), so P = 0 there.
+            if (qq0 < kw0 + 31 || qq0 + 31 >= a.T || kw0 + 31 >= a.T) {
+                const int vlo = key - qq0 - 4 * hi;
+                const int vhi = key < a.T ? a.T - 1 - qq0 - 4 * hi : vlo - 1;
 #pragma unroll
-                for (int k2 = 0; k2 < 2; ++k2) {
-                    const int ks4 = 2 * qb + k2;
-                    const u32x4 pb = pack8<DT>(s, 8 * k2);
-                    const u32x4 db = pack8<DT>(dp, 8 * k2);
-#pragma unroll
-                    for (int mb = 0; mb < MB; ++mb)
-                        dvt[mb] = mfma32<DT>(perm_a(&sOt[buf][(32 * mb + (lane & 31)) * PT], ks4, hi), pb, dvt[mb]);
-#pragma unroll
-                    for (int rb = 0; rb < RB; ++rb)
-                        dkt[rb] = mfma32<DT>(perm_a(&sQt[buf][(32 * rb + (lane & 31)) * PT], ks4, hi), db, dkt[rb]);
+                for (int v = 0; v < 16; ++v) {
+                    const int qo = 8 * (v / 4) + (v % 4);
+                    if ((uint32_t)(qo - vlo) > (uint32_t)(vhi - vlo)) s[v] = -INFINITY;
                 }
             }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float p = fast_exp2(s[v]);
+                s[v] = p;
+                dp[v] *= p;
+            }
+            // dV^T += dO^T P and dK^T += Q^T dS, the row-direction operands read transposed
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                const u32x4 pb = pack8<DT>(s, 8 * k2);
+                const u32x4 db = pack8<DT>(dp, 8 * k2);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+                    dvt[mb] = mfma32<DT>(tr_operand<D>(sO[buf], 32 * qb + 16 * k2, 32 * mb, lane), pb, dvt[mb]);
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+                    dkt[rb] = mfma32<DT>(tr_operand<R>(sQ[buf], 32 * qb + 16 * k2, 32 * rb, lane), db, dkt[rb]);
+            }
         }
-        if (more) put(buf ^ 1);
+        if (more) put(buf ^ 1, q0 + BQ);
         __syncthreads();
-    }
+    };
+    fetch(0, k0);
+    put(0, k0);
+    __syncthreads();
+    for (int q0 = k0, buf = 0; q0 < a.T; q0 += BQ, buf ^= 1) tile(buf, q0);
     if (key >= a.T) return;
-    // dV^T / dK^T: lane = key, rows 8(v/4) + 4hi + v%4 of each 32-row block
+    // dV^T / dK^T: lane = key, rows 8(v/4) + 4hi + v%4 of each 32-row block,
+    // i.e. runs of four consecutive columns of the key's gradient rows
     in_t *dvr = (in_t *)a.dv + b * a.dv_sb + h * a.dv_sh + (int64_t)key * a.dv_st;
     in_t *dkr = (in_t *)a.dk + b * a.dk_sb + h * a.dk_sh + (int64_t)key * a.dk_st;
+    if (a.dv_accumulate) {
+        Run4<DT> prev[MB][4];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int d = 32 * mb + 8 * (v / 4) + 4 * hi + (v % 4);
-            float x = dvt[mb][v];
-            if (a.dv_accumulate) x += to_f32<DT>(dvr[d]);
-            dvr[d] = from_f32<DT>(x);
-        }
+            for (int g = 0; g < 4; ++g) prev[mb][g] = Run4<DT>::load(dvr + 32 * mb + 8 * g + 4 * hi);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float x[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[e] = dvt[mb][4 * g + e] + prev[mb][g].get(e);
+                Run4<DT>::store(dvr + 32 * mb + 8 * g + 4 * hi, x);
+            }
+    } else {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float x[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[e] = dvt[mb][4 * g + e];
+                Run4<DT>::store(dvr + 32 * mb + 8 * g + 4 * hi, x);
+            }
+    }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int d = 32 * rb + 8 * (v / 4) + 4 * hi + (v % 4);
-            if (d < R) dkr[d] = from_f32<DT>(dkt[rb][v] * a.sm_scale);
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * rb + 8 * g + 4 * hi;
+            if (d >= R) continue;
+            float x[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = dkt[rb][4 * g + e] * a.sm_scale;
+            Run4<DT>::store(dkr + d, x);
         }
 }
 
 template <int DT, int R, int D>
-__global__ __launch_bounds__(NT, (DT != HOFA_F32 && D == 64 && R <= 32) ? 4 : 1) void attn_bwd_dq_kernel(AttnBwdK a) {
+__global__ __launch_bounds__(NT, (dq_occupancy<DT, R, D>())) void attn_bwd_dq_kernel(AttnBwdK a) {
     using in_t = typename Stor<DT>::type;
+    using LK = TileL<R>;
+    using LV = TileL<D>;
     constexpr int KS = R / 16, DKS = D / 16;
     constexpr int RB = (R + 31) / 32;
-    constexpr int PK = R + 8, PV = D + 8, PT = BN + 4;
     constexpr bool SPL = DT == HOFA_F32;
-    __shared__ __attribute__((aligned(16))) uint16_t sK[2][BN * PK];
-    __shared__ __attribute__((aligned(16))) uint16_t sKlo[2][SPL ? BN * PK : 8];
-    __shared__ __attribute__((aligned(16))) uint16_t sKt[2][RB * 32 * PT];
-    __shared__ __attribute__((aligned(16))) uint16_t sV[2][BN * PV];
+    __shared__ __attribute__((aligned(16))) uint16_t sK[2][LK::ELEMS];
+    __shared__ __attribute__((aligned(16))) uint16_t sKlo[2][SPL ? LK::ELEMS : 8];
+    __shared__ __attribute__((aligned(16))) uint16_t sV[2][LV::ELEMS];
 
     const int nq = (a.T + BM - 1) / BM;
     int bh, qb;
-    xcd_remap(blockIdx.x, nq, a.B * a.H, &bh, &qb);
+    xcd_rank_remap(blockIdx.x, nq, a.B * a.H, &bh, &qb);
+    qb = nq - 1 - qb;  // the last query blocks have the most work
     const int b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x, lane = tid & 63, hi = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -294,20 +470,20 @@ __global__ __launch_bounds__(NT, (DT != HOFA_F32 && D == 64 && R <= 32) ? 4 : 1)
     const in_t *kp = (const in_t *)a.k + b * a.k_sb + h * a.k_sh;
     const in_t *vp = (const in_t *)a.v + b * a.v_sb + h * a.v_sh;
     const in_t *op = (const in_t *)a.dO + b * a.o_sb + h * a.o_sh;
-    u32x4 qop[KS], qlo[KS], oop[DKS];
+    // B operands: c Q as a hi/lo pair (k = dims), dO (k = dv) of this lane's
+    // query, and the shift k-step (-lse, -Dt) against ones
+    u32x4 qh[KS], ql[KS], oop[DKS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        qop[ks] = qrow < a.T ? load_op8<DT>(qp + (int64_t)qrow * a.q_st + 16 * ks + 8 * hi) : u32x4{0, 0, 0, 0};
-        if constexpr (SPL)
-            qlo[ks] = qrow < a.T ? load_lo8_f32((const float *)qp + (int64_t)qrow * a.q_st + 16 * ks + 8 * hi)
-                                 : u32x4{0, 0, 0, 0};
-    }
+    for (int ks = 0; ks < KS; ++ks)
+        load_scaled_op8<DT>(qp + (int64_t)qrow * a.q_st + 16 * ks + 8 * hi, a.c, qrow < a.T, qh[ks], ql[ks]);
 #pragma unroll
     for (int ks = 0; ks < DKS; ++ks)
         oop[ks] = qrow < a.T ? load_op8<DT>(op + (int64_t)qrow * a.o_st + 16 * ks + 8 * hi) : u32x4{0, 0, 0, 0};
     const float lq = qrow < a.T ? a.lse[(int64_t)bh * a.T + qrow] : 0.f;
     const float dq_t = qrow < a.T ? a.dt[(int64_t)bh * a.T + qrow] : 0.f;
-    for (int i = tid; i < 2 * RB * 32 * PT; i += NT) (&sKt[0][0])[i] = 0;
+    const u32x4 xb = {hi ? 0u : split_pair<DT>(-lq), 0u, 0u, 0u};
+    const u32x4 yb = {hi ? 0u : split_pair<DT>(-dq_t), 0u, 0u, 0u};
+    const u32x4 ones = {hi ? 0u : kOnes2<DT>, 0u, 0u, 0u};
 
     f32x16 dqt[RB];
 #pragma unroll
@@ -315,71 +491,98 @@ __global__ __launch_bounds__(NT, (DT != HOFA_F32 && D == 64 && R <= 32) ? 4 : 1)
 #pragma unroll
         for (int v = 0; v < 16; ++v) dqt[rb][v] = 0.f;
 
-    RowStage<DT, R> stk;
-    RowStage<DT, D> stv;
+    TileStage<DT, R> stk;
+    TileStage<DT, D> stv;
     const int kend = min(a.T, q0 + BM);
-    stk.fetch(kp, a.k_st, 0, a.T);
-    stv.fetch(vp, a.v_st, 0, a.T);
-    __syncthreads();  // pad rows of K^T cleared
-    stk.template put<PK, PT, true, true>(sK[0], sKt[0], sKlo[0]);
-    stv.template put<PV, PT, true, false>(sV[0], nullptr, nullptr);
+    if constexpr (SPL) {
+        stk.fetch(kp, a.k_st, 0, a.T);
+        stv.fetch(vp, a.v_st, 0, a.T);
+        stk.put(sK[0], sKlo[0]);
+        stv.put(sV[0], nullptr);
+    } else {
+        TileDma<R>::fetch(sK[0], kp, a.k_st, 0, a.T, w, lane);
+        TileDma<D>::fetch(sV[0], vp, a.v_st, 0, a.T, w, lane);
+        wait_vmem();
+    }
     __syncthreads();
-    int buf = 0;
-    for (int k0 = 0; k0 < kend; k0 += BN, buf ^= 1) {
+    auto tile = [&](int buf, int k0) {
         const bool more = k0 + BN < kend;
         if (more) {
-            stk.fetch(kp, a.k_st, k0 + BN, a.T);
-            stv.fetch(vp, a.v_st, k0 + BN, a.T);
+            if constexpr (SPL) {
+                stk.fetch(kp, a.k_st, k0 + BN, a.T);
+                stv.fetch(vp, a.v_st, k0 + BN, a.T);
+            } else {
+                TileDma<R>::fetch(sK[buf ^ 1], kp, a.k_st, k0 + BN, a.T, w, lane);
+                TileDma<D>::fetch(sV[buf ^ 1], vp, a.v_st, k0 + BN, a.T, w, lane);
+            }
         }
-        if (k0 <= qw0 + 31) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                f32x16 s = {}, dp = {};
-                const uint16_t *krow = &sK[buf][(32 * kb + (lane & 31)) * PK];
+        for (int kb = 0; kb < 2; ++kb) {
+            const int kk0 = k0 + 32 * kb;
+            if (kk0 > qw0 + 31) continue;  // every key of the block follows this wave's queries
+            const int rk = 32 * kb + (lane & 31);
+            // this block's key rows: every row operand read is issued before the products
+            u32x4 ka[KS], kla[SPL ? KS : 1], va[DKS];
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    const u32x4 ka = *(const u32x4 *)(krow + 16 * ks + 8 * hi);
-                    s = mfma32<DT>(ka, qop[ks], s);
-                    if constexpr (SPL) {
-                        s = mfma32<DT>(ka, qlo[ks], s);
-                        s = mfma32<DT>(*(const u32x4 *)(&sKlo[buf][(32 * kb + (lane & 31)) * PK] + 16 * ks + 8 * hi),
-                                       qop[ks], s);
-                    }
-                }
-                const uint16_t *vrow = &sV[buf][(32 * kb + (lane & 31)) * PV];
+            for (int ks = 0; ks < KS; ++ks) {
+                ka[ks] = *(const u32x4 *)&sK[buf][LK::off(rk, 16 * ks + 8 * hi)];
+                if constexpr (SPL) kla[ks] = *(const u32x4 *)&sKlo[buf][LK::off(rk, 16 * ks + 8 * hi)];
+            }
 #pragma unroll
-                for (int ks = 0; ks < DKS; ++ks) dp = mfma32<DT>(*(const u32x4 *)(vrow + 16 * ks + 8 * hi), oop[ks], dp);
-                const bool edge = k0 + 32 * kb + 31 > qw0 || k0 + 32 * kb + 31 >= a.T;
-                const int lim = min(qrow, a.T - 1) - k0 - 32 * kb - 4 * hi;  // key offset visible iff <= lim
+            for (int ks = 0; ks < DKS; ++ks) va[ks] = *(const u32x4 *)&sV[buf][LV::off(rk, 16 * ks + 8 * hi)];
+            // S'^T = c K Q^T - lse and dP'^T = V dO^T - Dt in C[key, query]
+            f32x16 s = {}, dp = {};
+            sched_reads_then_mfma<KS * (SPL ? 3 : 2) + 1, DKS + 1>();
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    float p = fast_exp2(fmaf(s[v], a.c, -lq));
-                    if (edge) p = 8 * (v / 4) + (v % 4) <= lim ? p : 0.f;
-                    dp[v] = p * (dp[v] - dq_t);
-                }
+            for (int ks = 0; ks < KS; ++ks) {
+                s = mfma32<DT>(ka[ks], qh[ks], s);
+                s = mfma32<DT>(ka[ks], ql[ks], s);
+                if constexpr (SPL) s = mfma32<DT>(kla[ks], qh[ks], s);
+            }
+            s = mfma32<DT>(ones, xb, s);
 #pragma unroll
-                for (int k2 = 0; k2 < 2; ++k2) {
-                    const u32x4 db = pack8<DT>(dp, 8 * k2);
+            for (int ks = 0; ks < DKS; ++ks) dp = mfma32<DT>(va[ks], oop[ks], dp);
+            dp = mfma32<DT>(ones, yb, dp);
+            // blocks on the diagonal or past T: logits of keys past min(query, T-1) -> -inf
+            if (kk0 + 31 > qw0 || kk0 + 31 >= a.T) {
+                const int lim = min(qrow, a.T - 1) - kk0 - 4 * hi;  // key offset visible iff <= lim
 #pragma unroll
-                    for (int rb = 0; rb < RB; ++rb)
-                        dqt[rb] = mfma32<DT>(perm_a(&sKt[buf][(32 * rb + (lane & 31)) * PT], 2 * kb + k2, hi), db, dqt[rb]);
-                }
+                for (int v = 0; v < 16; ++v)
+                    if (8 * (v / 4) + (v % 4) > lim) s[v] = -INFINITY;
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) dp[v] *= fast_exp2(s[v]);
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                const u32x4 db = pack8<DT>(dp, 8 * k2);
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+                    dqt[rb] = mfma32<DT>(tr_operand<R>(sK[buf], 32 * kb + 16 * k2, 32 * rb, lane), db, dqt[rb]);
             }
         }
         if (more) {
-            stk.template put<PK, PT, true, true>(sK[buf ^ 1], sKt[buf ^ 1], sKlo[buf ^ 1]);
-            stv.template put<PV, PT, true, false>(sV[buf ^ 1], nullptr, nullptr);
+            if constexpr (SPL) {
+                stk.put(sK[buf ^ 1], sKlo[buf ^ 1]);
+                stv.put(sV[buf ^ 1], nullptr);
+            } else {
+                wait_vmem();
+            }
         }
         __syncthreads();
-    }
+    };
+    for (int k0 = 0, buf = 0; k0 < kend; k0 += BN, buf ^= 1) tile(buf, k0);
     if (qrow >= a.T) return;
     in_t *dqr = (in_t *)a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)qrow * a.dq_st;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int d = 32 * rb + 8 * (v / 4) + 4 * hi + (v % 4);
-            if (d < R) dqr[d] = from_f32<DT>(dqt[rb][v] * a.sm_scale);
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * rb + 8 * g + 4 * hi;
+            if (d >= R) continue;
+            float x[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = dqt[rb][4 * g + e] * a.sm_scale;
+            Run4<DT>::store(dqr + d, x);
         }
 }
 

@@ -177,4 +177,20 @@ __device__ __forceinline__ void xcd_remap(int blk, int nrow, int nhead, int *hea
     }
 }
 
+// Longest-first variant for kernels whose blocks carry unequal causal work:
+// blocks of one head stay on one XCD, and each XCD takes the work rank
+// (0 = most work) as the outer index over its heads, so every XCD dispatches
+// all of its longest blocks before any shorter one.
+__device__ __forceinline__ void xcd_rank_remap(int blk, int nrank, int nhead, int *head, int *rank) {
+    constexpr int kXcd = 8;
+    if (nhead % kXcd == 0) {
+        const int xcd = blk % kXcd, slot = blk / kXcd, hpx = nhead / kXcd;
+        *rank = slot / hpx;
+        *head = (slot % hpx) * kXcd + xcd;
+    } else {
+        *rank = blk / nhead;
+        *head = blk % nhead;
+    }
+}
+
 }  // namespace hofa
