@@ -119,7 +119,11 @@ class HybridOutlierFactorizedAttention(nn.Module):
         if self.forced_mha_heads > 0 or self.pure_mha_low_rank_k or self.r == self.d_head:
             return self._forward_attention_only(Q, K, V)
         gate_logits, mix_g = self._compute_gates_optimized(Q, K)
-        self.last_mix_g = mix_g.detach() if mix_g is not None else None
+        if not torch.compiler.is_compiling():
+            # gate telemetry (written, never read by the reference's training); a
+            # module attribute set inside a checkpointed block would break the
+            # compiled graph, so traced runs leave it unchanged
+            self.last_mix_g = mix_g.detach() if mix_g is not None else None
         log_gamma = F.logsigmoid(-gate_logits).squeeze(-1)
         log_alpha = self.log_alpha if self.learnable_alpha else None
         if self.r == 0:
@@ -129,6 +133,9 @@ class HybridOutlierFactorizedAttention(nn.Module):
         if getattr(self, "rotary_emb", None) is not None:
             cos, sin = self.rotary_emb(N)
             Q_O, K_O = apply_rotary_pos_emb(Q[..., :self.r], K[..., :self.r], cos, sin)
+            # the float32 tables promote 16-bit Q/K; the reference's SDPA runs
+            # them in the autocast dtype (that of V), and so does the core
+            Q_O, K_O = Q_O.to(V.dtype), K_O.to(V.dtype)
         sm_scale = ((self.d_head / self.r) ** 0.5) * self.attention_scale
         Y = hofa_core(Q_O, K_O, Q, K, V, log_gamma, log_alpha, mix_g.squeeze(-1), self.gla_scale, self.r, sm_scale)
         return self._merge(Y)
