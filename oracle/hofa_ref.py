@@ -380,6 +380,53 @@ class HOFARef:
             return out, (K[..., :self.r].contiguous(), V.contiguous()), S
         return out
 
+    # -- the non-hybrid variants ------------------------------------------
+    def _rope_full(self, Q, K, n0, n1):
+        """RoPE over all ``d_h`` channels (the rotary module's dim is ``d_h``
+        when ``r`` is 0 or ``d_h``: Infer :57-61, Train :77-81)."""
+        cos, sin = rope_tables(self.dh, n1, self.rope_base)
+        cos, sin = cos[n0:n1].to(self.dtype), sin[n0:n1].to(self.dtype)
+        return apply_rope(Q, cos, sin), apply_rope(K, cos, sin)
+
+    def _pure_gla(self, Q, K, V, gate_w, gate_b, gla_scale, log_alpha=None, eps: float = FP32_EPS, S0=None):
+        """``gla_scale * RMSNorm(GLA(Q, K, V, g))`` over all ``d_h`` channels with
+        ``log_gamma = logsigmoid(-(Q w_q + K w_k + b))`` (Infer :146-159,
+        Train :201-223; ``g`` carries ``exp(log_alpha)`` when given)."""
+        a, _ = compute_gates(Q, K, gate_w, gate_b)
+        g = decay_from_gates(F.logsigmoid(-a), self.dh, log_alpha)
+        y, S = gla_chunked(Q, K, V, g, chunk=self.chunk, S0=S0)
+        return rmsnorm(y, eps) * gla_scale.reshape(1, -1, 1, self.dh).to(y.dtype), S
+
+    def forward_variant(self, x, mha_heads: int = 0, scale: float = 1.0, use_alpha: bool = False,
+                        eps: float = FP32_EPS):
+        """Prefill of the non-hybrid configurations, returning ``(out, S)``:
+
+        * ``r == 0``: the pure normalized GLA on every head (``mha_heads`` = 0);
+        * ``r == d_h``: causal softmax attention on every head with RoPE on all
+          channels and logit scale ``scale`` (``mha_heads`` = H; Infer :161-171
+          with 1.0, Train :225-231 with ``attention_scale``);
+        * width split (Infer :106-143, Train :139-175): heads ``[0, mha_heads)``
+          as above, the rest the pure GLA with their rows of ``gate_proj``,
+          ``gla_scale`` (and ``log_alpha`` when ``use_alpha``).
+        ``S`` is the GLA heads' final state ``[B, H - mha_heads, d_h, d_h]``.
+        """
+        Q, K, V = self._qkv(x)
+        N, m = x.shape[1], mha_heads
+        parts, S = [], None
+        if m > 0:
+            Qm, Km = Q[:, :m], K[:, :m]
+            if self.use_rope:
+                Qm, Km = self._rope_full(Qm, Km, 0, N)
+            parts.append(outlier_attention(Qm, Km, V[:, :m], scale))
+        if m < self.H:
+            la = self._log_alpha()
+            la = la.reshape(1, self.H, 1, self.dh)[:, m:] if (use_alpha and la is not None) else None
+            y, S = self._pure_gla(Q[:, m:], K[:, m:], V[:, m:], self.p["gate_proj.weight"][m:],
+                                  self.p["gate_proj.bias"][m:], self._gla_scale().reshape(1, self.H, 1, -1)[:, m:],
+                                  la, eps)
+            parts.append(y)
+        return self._out(self._rd(torch.cat(parts, 1))), S
+
     # -- decode (Train forward_step semantics, :298-438) -----------------
     def forward_step(self, x, cache_O=None, state=None, eps: float = FP32_EPS):
         """One token.  ``cache_O`` is ``(K_cache [B,H,L,r], V_cache [B,H,L,d_h])``

@@ -116,7 +116,9 @@ class HybridOutlierFactorizedAttention(nn.Module):
     def forward(self, x):
         B, N, D = x.shape
         Q, K, V = self._project(x)
-        if self.forced_mha_heads > 0 or self.pure_mha_low_rank_k or self.r == self.d_head:
+        if self.forced_mha_heads > 0:
+            return self._forward_width_split(Q, K, V)
+        if self.pure_mha_low_rank_k or self.r == self.d_head:
             return self._forward_attention_only(Q, K, V)
         gate_logits, mix_g = self._compute_gates_optimized(Q, K)
         if not torch.compiler.is_compiling():
@@ -140,12 +142,36 @@ class HybridOutlierFactorizedAttention(nn.Module):
         Y = hofa_core(Q_O, K_O, Q, K, V, log_gamma, log_alpha, mix_g.squeeze(-1), self.gla_scale, self.r, sm_scale)
         return self._merge(Y)
 
-    def _forward_attention_only(self, Q, K, V):
-        """Ablations without the hybrid blend (:139-231): width split, reduced-QK
-        MHA and r == d_head.  PyTorch SDPA as in the reference."""
+    def _forward_width_split(self, Q, K, V):
+        """Width-split ablation (:139-175): the first ``mha_heads_for_width_split``
+        heads run causal softmax attention over the full head (RoPE'd, scale
+        ``attention_scale``, PyTorch SDPA as in the reference), the rest the
+        normalized GLA over all ``d_head`` channels (the ``r = 0`` core on the
+        HIP kernels) with their rows of ``gate_proj`` and ``gla_scale``.  With
+        ``learnable_alpha`` the GLA heads take their own rows of ``log_alpha``
+        (the reference multiplies the GLA heads' decay by all heads' alphas,
+        which only broadcasts when no head is split off)."""
         B, H, N, d = Q.shape
-        if self.forced_mha_heads > 0:
-            raise NotImplementedError("the width-split ablation is not provided by this build")
+        m = self.forced_mha_heads
+        Q_mha, Q_gla = Q[:, :m], Q[:, m:]
+        K_mha, K_gla = K[:, :m], K[:, m:]
+        V_mha, V_gla = V[:, :m], V[:, m:]
+        if getattr(self, "rotary_emb", None) is not None:
+            cos, sin = self.rotary_emb(N)
+            Q_mha, K_mha = apply_rotary_pos_emb(Q_mha, K_mha, cos, sin)
+        Y_mha = F.scaled_dot_product_attention(Q_mha.to(V.dtype), K_mha.to(V.dtype), V_mha, is_causal=True,
+                                               scale=self.attention_scale)
+        W_g = self.gate_proj.weight
+        gate_logits = self._gate_terms(Q_gla, K_gla, W_g[m:], self.gate_proj.bias[m:])
+        log_gamma = F.logsigmoid(-gate_logits)
+        log_alpha = self.log_alpha[:, m:] if self.learnable_alpha else None
+        Y_gla = hofa_core(None, None, Q_gla, K_gla, V_gla, log_gamma, log_alpha, None, self.gla_scale[:, m:], 0, 1.0)
+        return self._merge(torch.cat([Y_mha.to(Y_gla.dtype), Y_gla], dim=1))
+
+    def _forward_attention_only(self, Q, K, V):
+        """Ablations without the hybrid blend (:176-231): reduced-QK MHA and
+        r == d_head.  PyTorch SDPA as in the reference."""
+        B, H, N, d = Q.shape
         if self.pure_mha_low_rank_k:
             Q, K = Q[..., :self.r], K[..., :self.r]
             scale = ((self.d_head / self.r) ** 0.5) * self.attention_scale
@@ -205,7 +231,8 @@ class HybridOutlierFactorizedAttention(nn.Module):
             Y = (self.inlier_norm(Y.float()) * self.gla_scale).to(Q.dtype)
             return self._merge(Y), None, S
         if self.forced_mha_heads > 0:
-            raise NotImplementedError("the width-split ablation is not provided by this build")
+            # the reference's forward_step has no width-split branch either
+            raise NotImplementedError("forward_step does not support the width-split ablation")
         if self.pure_mha_low_rank_k:
             Qr, Kr = Q[..., :self.r], K[..., :self.r]
             scale = ((self.d_head / self.r) ** 0.5) * self.attention_scale
