@@ -19,7 +19,10 @@ is listed in the test files that exercise it:
   formulations checked against each other in float64, chunk-size independence,
   the scalar-decay special case, and golden vectors (decode recurrence).
 * ``decode_step``  -> golden vectors; equality with the last row of a prefill.
-* ``HOFARef``  -> golden vectors written by the reference's own Train module.
+* ``HOFARef``  -> golden vectors written by the reference's own Train module;
+  its ``forward_variant`` (r = 0, r = d_h, width split) -> tests/test_oracle_variants.py
+  (SDPA with RoPE on all channels, the GLA recurrence + ``nn.RMSNorm``, head
+  independence); given RoPE tables (YaRN) enter as they are.
 * ``layer_norm`` / ``gelu``  -> ``nn.LayerNorm`` / ``nn.GELU`` (library routines).
 * ``SubwordLMRef``  -> golden logits written by the reference's own Train
   ``SubwordLM`` (tests/golden/make_golden_lm.py); decode == last prefill row.
@@ -294,9 +297,12 @@ class HOFARef:
 
     def __init__(self, state: dict, d_model: int, num_heads: int, r: int, rope_base: float = 10000.0,
                  use_rope: bool = True, attention_scale: float = 1.0, chunk: int = 64,
-                 dtype=torch.float64, act_dtype=None, rope_f32_tables: bool = False):
+                 dtype=torch.float64, act_dtype=None, rope_f32_tables: bool = False, rope_tables=None):
         self.act = act_dtype
         self.rope_f32 = rope_f32_tables
+        # given (cos, sin) rows replace the computed tables (a context-extension
+        # patch such as YaRN, src/yarn.py:74-82, stores its own, in 16 bits)
+        self.rope_given = rope_tables
         self.p = {kk: vv.detach().to(dtype) for kk, vv in state.items()}
         if act_dtype is not None:  # weights enter the 16-bit ops rounded (a cast module or autocast)
             for kk in ("W_q.weight", "W_k.weight", "W_v.weight", "out_proj.weight", "gate_proj.weight",
@@ -334,6 +340,9 @@ class HOFARef:
                              self.p.get("fixed_mix"), **kw)
 
     def _rope(self, n0, n1):
+        if self.rope_given is not None:
+            cos, sin = self.rope_given
+            return cos[n0:n1].to(self.dtype), sin[n0:n1].to(self.dtype)
         cos, sin = rope_tables(self.r, n1, self.rope_base)
         cos, sin = cos[n0:n1].to(self.dtype), sin[n0:n1].to(self.dtype)
         if self.rope_f32:
@@ -483,7 +492,7 @@ class SubwordLMRef:
     """
 
     def __init__(self, state: dict, d_model: int, num_heads: int, r_list, rope_base: float = 10000.0,
-                 attn_eps: float = FP32_EPS, dtype=torch.float64, act_dtype=None):
+                 attn_eps: float = FP32_EPS, dtype=torch.float64, act_dtype=None, rope_tables=None):
         self.dtype = dtype
         self.act = act_dtype
         self.attn_eps = attn_eps
@@ -494,7 +503,8 @@ class SubwordLMRef:
             pre = f"layers.{i}."
             sub = {k[len(pre):]: v for k, v in state.items() if k.startswith(pre)}
             attn = HOFARef({k[len("attn."):]: v for k, v in sub.items() if k.startswith("attn.")}, d_model,
-                           num_heads, r, rope_base=rope_base, dtype=dtype, act_dtype=act_dtype)
+                           num_heads, r, rope_base=rope_base, dtype=dtype, act_dtype=act_dtype,
+                           rope_tables=None if rope_tables is None else rope_tables[i])
             t = {k: v.detach().to(dtype) for k, v in sub.items() if not k.startswith("attn.")}
             self.layers.append((attn, t))
 

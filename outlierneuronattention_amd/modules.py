@@ -31,12 +31,17 @@ class RotaryEmbedding(nn.Module):
         self.register_buffer("sin_cached", sin, persistent=False)
 
     def forward(self, seq_len: int):
-        """``(cos, sin)`` rows ``[0, seq_len)``; the tables grow when needed."""
+        """``(cos, sin)`` rows ``[0, seq_len)``; the tables grow when needed,
+        from the current ``inv_freq`` (which a context-extension patch such
+        as :func:`outlierneuronattention_amd.yarn.patch_model_yarn` may have
+        replaced), in float32 (src/modules/modules.py:19-26)."""
         if seq_len > self.max_seq_len_cached:
             self.max_seq_len_cached = seq_len
-            _, cos, sin = _tables(self.dim, seq_len, self.base, device=self.inv_freq.device)
-            self.register_buffer("cos_cached", cos, persistent=False)
-            self.register_buffer("sin_cached", sin, persistent=False)
+            pos = torch.arange(seq_len, dtype=torch.float32, device=self.inv_freq.device)
+            ang = torch.outer(pos, self.inv_freq)
+            full = torch.cat((ang, ang), dim=-1)
+            self.register_buffer("cos_cached", full.cos(), persistent=False)
+            self.register_buffer("sin_cached", full.sin(), persistent=False)
         return self.cos_cached[:seq_len], self.sin_cached[:seq_len]
 
 
