@@ -381,8 +381,188 @@ def cpu_baseline_decode(B: int, budget_s: float = 10.0):
         if (el >= budget_s and n >= 2) or n >= 10000:
             break
     return dict(value=B * n / el, unit="tok/s", cores=torch.get_num_threads(), kind="port",
+                cpu_count=os.cpu_count(), cpu_model=host_info()["cpu_model"],
                 sample=f"{n} decode steps of cfg3 at B={B} (H=16, d_h=64, r=16, L=32768) in fp32, "
                        f"oracle/hofa_ref.decode_step, {el:.1f} s")
+
+
+def host_info():
+    """The host the CPU legs run on: core count, CPU model and torch's thread count."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return dict(cpu_count=os.cpu_count(), cpu_model=model, torch_threads=torch.get_num_threads())
+
+
+def _median_time(fn, warmup: int = 3, reps: int = 5, budget_s: float = 20.0):
+    """Median wall time of ``fn`` over ``reps`` runs after ``warmup`` runs;
+    both counts shrink (to 1 and 3) when the budget would be exceeded."""
+    t0 = time.perf_counter()
+    fn()
+    one = time.perf_counter() - t0
+    if one * (warmup + reps) > budget_s:
+        warmup, reps = 1, 3
+    for _ in range(warmup - 1):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2], warmup, reps
+
+
+def _rand_layer_state(d_model, H, r, gen, alpha=False):
+    """Random parameters with the module's names (std 0.02 projections,
+    non-trivial gates) for the oracle's functional layer."""
+    dh = d_model // H
+    rn = lambda *sh, sd=1.0: torch.randn(*sh, generator=gen) * sd  # noqa: E731
+    st = {"W_q.weight": rn(d_model, d_model, sd=0.02), "W_k.weight": rn(d_model, d_model, sd=0.02),
+          "W_v.weight": rn(d_model, d_model, sd=0.02), "out_proj.weight": rn(d_model, d_model, sd=0.02),
+          "gate_proj.weight": rn(H, 2 * dh, sd=0.1), "gate_proj.bias": torch.full((H,), -1.0),
+          "mix_proj.weight": rn(H, 2 * dh, sd=0.1), "mix_proj.bias": torch.zeros(H),
+          "gla_scale": torch.ones(1, H, 1, dh)}
+    if alpha:
+        st["log_alpha"] = torch.zeros(1, H, 1, dh - r)
+    return st
+
+
+# cfg1: one fp32 layer, d_model 256, H=4, d_h=64, r=16, prefill 512 then 16 decode steps fed back
+C1_D, C1_H, C1_R, C1_T, C1_STEPS = 256, 4, 16, 512, 16
+
+
+def bench_cfg1(reps: int = 20):
+    """cfg1 on the GPU through the inference module (fp32): prefill of 512
+    tokens then 16 decode steps, each fed the layer's last output row."""
+    from outlierneuronattention_amd.config import ModelConfig
+    from outlierneuronattention_amd.HybridOutlierFactorizedAttention import HybridOutlierFactorizedAttention
+    torch.manual_seed(0)
+    m = HybridOutlierFactorizedAttention(ModelConfig(d_model=C1_D, num_heads=C1_H, num_layers=1, r=C1_R,
+                                                     device="cuda")).cuda().eval()
+    x = torch.randn(1, C1_T, C1_D, generator=torch.Generator().manual_seed(1)).cuda()
+
+    def run():
+        with torch.no_grad():
+            y, cache, state = m(x, return_state=True)
+            t = y[:, -1:]
+            for _ in range(C1_STEPS):
+                t, cache, state = m.forward_step(t, cache, state)
+        return t
+
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        run()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    return dict(workload="cfg1: one fp32 layer (d_model 256, H=4, d_h=64, r=16), prefill 512 + 16 decode steps "
+                         "fed back", ms_per_run=round(ms, 3), timing="host wall clock per run, eager launches")
+
+
+def cpu_cfg1():
+    """cfg1 on the host: the oracle layer (fp32) doing the same prefill and 16 fed-back steps."""
+    from oracle import hofa_ref as ref
+    gen = torch.Generator().manual_seed(0)
+    o = ref.HOFARef(_rand_layer_state(C1_D, C1_H, C1_R, gen), C1_D, C1_H, C1_R, dtype=torch.float32)
+    x = torch.randn(1, C1_T, C1_D, generator=gen)
+
+    def run():
+        with torch.no_grad():
+            y, cache, state = o.forward(x, return_state=True)
+            t = y[:, -1:]
+            for _ in range(C1_STEPS):
+                t, cache, state = o.forward_step(t, cache, state)
+
+    sec, w, n = _median_time(run)
+    return dict(value=round(sec * 1e3, 2), unit="ms per run", kind="port", cores=torch.get_num_threads(),
+                sample=f"the full cfg1 run (oracle HOFARef, fp32), {w} warm-up + median of {n}")
+
+
+def cpu_prefill(heads: int = 4):
+    """cfg2 attention core on the host (oracle hofa_core, fp32) over ``heads``
+    of the 64 (b, h) heads at full T=4096: TFLOP/s of the same algorithmic count."""
+    from oracle import hofa_ref as ref
+    gen = torch.Generator().manual_seed(4321)
+    q, k, v = (torch.randn(1, heads, P_T, P_D, generator=gen) for _ in range(3))
+    g = torch.clamp(F.logsigmoid(torch.randn(1, heads, P_T, P_J, generator=gen)) / 16, -5, 0)
+    mix = torch.sigmoid(torch.randn(1, heads, P_T, generator=gen))
+    gs = torch.ones(1, heads, 1, P_D)
+    with torch.no_grad():
+        sec, w, n = _median_time(lambda: ref.hofa_core(q, k, v, g, mix, gs, P_R, math.sqrt(P_D / P_R), eps=1e-5))
+    fl = prefill_flops(B=1, H=heads)
+    return dict(value=round(fl / sec / 1e12, 4), unit="TFLOP/s", kind="port", cores=torch.get_num_threads(),
+                sample=f"{heads} of the 64 heads of cfg2 at full T=4096 (fp32, oracle hofa_core), "
+                       f"{sec * 1e3:.0f} ms per call, {w} warm-up + median of {n}")
+
+
+def cpu_train(heads: int = 2):
+    """cfg4 attention core forward + backward on the host (float32 autograd of
+    the oracle) over ``heads`` of the 96 (b, h) heads at full T=2048."""
+    from oracle import hofa_ref as ref
+    gen = torch.Generator().manual_seed(777)
+    q, k, v = (torch.randn(1, heads, T_T, T_D, generator=gen).requires_grad_() for _ in range(3))
+    J = T_D - T_R
+    lg = torch.full((1, heads, T_T), -1.0)
+    la = torch.log(-F.logsigmoid(2 + 4 * torch.rand(1, heads, 1, J, generator=gen))).requires_grad_()
+    mix = torch.sigmoid(torch.randn(1, heads, T_T, generator=gen)).requires_grad_()
+    gs = torch.ones(1, heads, 1, T_D, requires_grad=True)
+    dy = torch.randn(1, heads, T_T, T_D, generator=gen)
+
+    def step():
+        y, _ = ref.hofa_core(q, k, v, ref.decay_from_gates(lg, J, la), mix, gs, T_R, math.sqrt(T_D / T_R))
+        y.backward(dy)
+
+    sec, w, n = _median_time(step)
+    fwd, bwd = train_flops(B=1, H=heads)
+    return dict(value=round((fwd + bwd) / sec / 1e12, 4), unit="TFLOP/s", kind="port",
+                cores=torch.get_num_threads(),
+                sample=f"{heads} of the 96 heads of cfg4 at full T=2048 (fp32 autograd of oracle hofa_core), "
+                       f"{sec * 1e3:.0f} ms per step, {w} warm-up + median of {n}")
+
+
+def cpu_model(T: int = 1024, steps: int = 8):
+    """cfg5 on the host at reduced length: the 24-layer oracle LM (fp32,
+    random weights) prefills T ids, then decodes ``steps`` greedy tokens."""
+    from oracle import hofa_ref as ref
+    gen = torch.Generator().manual_seed(5)
+    sd = {}
+    for i in range(M_LAYERS):
+        for kk, vv in _rand_layer_state(M_D, M_H, M_R, gen).items():
+            sd[f"layers.{i}.attn.{kk}"] = vv
+        for nm, shape in (("ln_1", (M_D,)), ("ln_2", (M_D,))):
+            sd[f"layers.{i}.{nm}.weight"] = torch.ones(*shape)
+            sd[f"layers.{i}.{nm}.bias"] = torch.zeros(*shape)
+        sd[f"layers.{i}.mlp.0.weight"] = torch.randn(4 * M_D, M_D, generator=gen) * 0.02
+        sd[f"layers.{i}.mlp.0.bias"] = torch.zeros(4 * M_D)
+        sd[f"layers.{i}.mlp.2.weight"] = torch.randn(M_D, 4 * M_D, generator=gen) * 0.02
+        sd[f"layers.{i}.mlp.2.bias"] = torch.zeros(M_D)
+    sd["lm_head.weight"] = torch.randn(M_VOCAB, M_D, generator=gen) * 0.02
+    sd["ln_f.weight"], sd["ln_f.bias"] = torch.ones(M_D), torch.zeros(M_D)
+    o = ref.SubwordLMRef(sd, M_D, M_H, [M_R] * M_LAYERS, dtype=torch.float32)
+    ids = torch.randint(0, M_VOCAB, (1, T), generator=gen)
+    with torch.no_grad():
+        t0 = time.perf_counter()
+        logits, caches, states = o.forward(ids, return_state=True, last_only=True)
+        pre = time.perf_counter() - t0
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            logits, caches, states = o.forward_step(tok, caches, states)
+            tok = logits[:, -1].argmax(-1, keepdim=True)
+        dec = (time.perf_counter() - t0) / steps
+    return dict(value=round(1.0 / dec, 3), unit="tok/s (decode)", kind="port", cores=torch.get_num_threads(),
+                prefill_tok_per_s=round(T / pre, 1),
+                sample=f"cfg5 reduced to a {T}-token prompt (from 65536), B=1, 24 layers, fp32 oracle LM "
+                       f"(random weights): prefill once, then {steps} greedy steps")
 
 
 def calibrate_copy(nbytes: int = 1 << 30, reps: int = 20):
@@ -425,7 +605,7 @@ def main():
     ap.add_argument("--batch", type=int, default=4, help="batch of the headline decode line")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "train", "model", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "train", "model", "copy", "cpu"], default="all",
                     help="run one leg and print its result (profiling runs); default: the full line")
     ap.add_argument("--eager", action="store_true", help="decode with plain launches instead of graph replay")
     args = ap.parse_args()
@@ -433,6 +613,11 @@ def main():
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the multi-GPU "
               "layout is a design note, not a measured path.", file=sys.stderr)
         sys.exit(2)
+    if args.only == "cpu":  # the host legs alone (no GPU needed)
+        res = dict(host=host_info(), cfg1=cpu_cfg1(), cfg2=cpu_prefill(), cfg3=cpu_baseline_decode(args.batch, 2.0),
+                   cfg4=cpu_train(), cfg5=cpu_model())
+        print(json.dumps({"only": "cpu", "result": res}), flush=True)
+        return
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
@@ -463,7 +648,14 @@ def main():
             model[f"B{mb}"] = bench_model(mb)
         except Exception as e:  # the headline line must still print
             model[f"B{mb}"] = {"error": f"{type(e).__name__}: {e}"[:300]}
-    cpu = None if args.skip_cpu else cpu_baseline_decode(args.batch, args.cpu_budget)
+    cfg1 = bench_cfg1()
+    cpu = None
+    if not args.skip_cpu:
+        cpu = cpu_baseline_decode(args.batch, args.cpu_budget)
+        cfg1["cpu_baseline"] = cpu_cfg1()
+        prefill["cpu_baseline"] = cpu_prefill()
+        train["cpu_baseline"] = cpu_train()
+        model["cpu_baseline"] = cpu_model()
     achieved = head["gbs"]
     line = {
         "metric": "decode tok/s (split-K HOFA decode, 32k ctx)",
@@ -489,6 +681,8 @@ def main():
         "decode": {f"B{head['B']}": {k: round(v, 4) if isinstance(v, float) else v for k, v in head.items()},
                    f"B{side['B']}": {k: round(v, 4) if isinstance(v, float) else v for k, v in side.items()},
                    "B1_llc_resident": {k: round(v, 3) if isinstance(v, float) else v for k, v in hot.items()}},
+        "host": host_info(),
+        "cfg1": cfg1,
         "prefill_fwd": prefill,
         "train_fwd_bwd": train,
         "model_cfg5": dict(workload="cfg5: 24-layer SubwordLM (d_model 1024, H=16, d_h=64, r=16, vocab 50304, bf16, "

@@ -175,7 +175,10 @@ def _(dy, q_o, k_o, q, k, v, log_gamma, log_alpha, mix, gla_scale, n, rstd, chun
 # -------------------------------------------------------------------- autograd
 def _setup_context(ctx, inputs, output):
     q, k, v, log_gamma, log_alpha, mix, gla_scale, q_o, k_o, r, sm_scale, save = inputs
-    _, _, n, rstd, cs, o, lse = output
+    _, states, n, rstd, cs, o, lse = output
+    # only Y carries a gradient: no zero tensors for the other outputs' gradients
+    ctx.set_materialize_grads(False)
+    ctx.mark_non_differentiable(states, n, rstd, cs, o, lse)
     if not save:
         ctx.r = None
         return
@@ -186,6 +189,8 @@ def _setup_context(ctx, inputs, output):
 def _backward(ctx, dy, *_):
     if ctx.r is None:
         raise RuntimeError("hofa::prefill_fwd was run with save=False; call it with save=True to differentiate")
+    if dy is None:
+        return (None,) * 12
     q_o, k_o, q, k, v, log_gamma, log_alpha, mix, gla_scale, n, rstd, cs, o, lse = ctx.saved_tensors
     dq_o, dk_o, dq, dk, dv, d_lg, d_la, d_mix, d_gs = torch.ops.hofa.prefill_bwd(
         dy, q_o, k_o, q, k, v, log_gamma, log_alpha, mix, gla_scale, n, rstd, cs, o, lse, ctx.r, ctx.sm_scale)
