@@ -191,10 +191,15 @@ int hofa_attn_fwd(const hofa_attn_fwd_args_t *args, void *stream);
  *                  gate, saved for hofa_gla_bwd (needs fuse_norm_gate)
  *   rstd           float32 [B*H*T] receiving 1/sqrt(mean(Y_I^2) + eps) when
  *                  n_out is given
+ *   round_operands 0: matrix-core operands are split hi/lo bf16 pairs for
+ *                  every input dtype, so the result tracks an fp32
+ *                  computation.  1 (bf16/f16 inputs, no chunk_states): each
+ *                  operand of the in-chunk and inter-chunk products and the
+ *                  entering state are rounded to bf16 once, as the reference
+ *                  kernel rounds its dot operands (src/chunk_gla_inlier.py:96-121);
+ *                  ignored for f32 inputs.
  * Supported: D in {64, 128}, J = D - R a multiple of 16.  Decay per token
- * must be <= 0 (log of a factor in (0, 1]).  Matrix-core operands are split
- * hi/lo bf16 pairs for every input dtype, so the result tracks an fp32
- * computation.
+ * must be <= 0 (log of a factor in (0, 1]).
  * ---------------------------------------------------------------------- */
 typedef struct {
     int32_t B, H, T, D, R;
@@ -209,6 +214,8 @@ typedef struct {
     void *chunk_states;
     hofa_view_t n_out;
     float *rstd;
+    int32_t round_operands;
+    int32_t reserved;
 } hofa_gla_fwd_args_t;
 
 size_t hofa_gla_fwd_workspace_bytes(const hofa_gla_fwd_args_t *args);

@@ -61,7 +61,8 @@ class GlaFwdArgs(ctypes.Structure):
                 ("mix", View), ("gla_scale", View),
                 ("y", View), ("state_out", View),
                 ("chunk_states", ctypes.c_void_p),
-                ("n_out", View), ("rstd", ctypes.c_void_p)]
+                ("n_out", View), ("rstd", ctypes.c_void_p),
+                ("round_operands", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 class AttnBwdArgs(ctypes.Structure):

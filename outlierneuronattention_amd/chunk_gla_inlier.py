@@ -26,7 +26,7 @@ def chunk_states_numel(B: int, H: int, T: int, D: int, J: int) -> int:
 
 
 def gla_fwd_args(Q, K, V, log_gamma, r, log_alpha, mix_g, gla_scale, y, state_view, g, eps, chunk_states,
-                 n_out=None, rstd=None):
+                 n_out=None, rstd=None, round_operands=False):
     B, H, T, D = Q.shape
     r = int(r)
     J = D - r
@@ -35,6 +35,7 @@ def gla_fwd_args(Q, K, V, log_gamma, r, log_alpha, mix_g, gla_scale, y, state_vi
     a = _lib.GlaFwdArgs()
     a.B, a.H, a.T, a.D, a.R = B, H, T, D, r
     a.eps = float(eps)
+    a.round_operands = 1 if round_operands else 0
     a.q, a.k, a.v, a.y = _lib.view(Q), _lib.view(K), _lib.view(V), _lib.view(y)
     keep = []
     if g is not None:
@@ -73,7 +74,8 @@ def gla_fwd_args(Q, K, V, log_gamma, r, log_alpha, mix_g, gla_scale, y, state_vi
 def chunk_gla_inlier_fwd(Q, K, V, log_gamma, r, chunk_size, log_alpha=None, mix_g=None, gla_scale=None, out=None,
                          states_in=None, requires_grad=False, *, g: Optional[torch.Tensor] = None,
                          eps: float = 1e-5, chunk_states: Optional[torch.Tensor] = None,
-                         n_out: Optional[torch.Tensor] = None, rstd: Optional[torch.Tensor] = None):
+                         n_out: Optional[torch.Tensor] = None, rstd: Optional[torch.Tensor] = None,
+                         round_operands: bool = False):
     """Chunked GLA over channels ``[r, d_head)``; returns ``(Y, states_out)``.
 
     Same contract as the reference (src/chunk_gla_inlier.py:153-237):
@@ -87,7 +89,11 @@ def chunk_gla_inlier_fwd(Q, K, V, log_gamma, r, chunk_size, log_alpha=None, mix_
     ``chunk_states`` (16-bit, ``chunk_states_numel(...)`` elements) receives
     the state entering every chunk as hi/lo operand pairs, ``n_out``
     (``[B,H,T,d_head]``, dtype of Q) ``RMSNorm(Y_I)`` and ``rstd`` (float32,
-    ``B*H*T``) the per-token reciprocal RMS.
+    ``B*H*T``) the per-token reciprocal RMS.  By default every matrix-product
+    operand is a hi/lo bf16 pair, which tracks an fp32 computation;
+    ``round_operands`` (bf16/f16 inputs, no ``chunk_states``) rounds each
+    operand and the carried state to bf16 once, as the reference kernel does
+    (src/chunk_gla_inlier.py:96-121), with the reference's larger error.
     """
     if requires_grad or states_in is not None:
         raise NotImplementedError("per-chunk state export through states_in is not supported; "
@@ -104,8 +110,10 @@ def chunk_gla_inlier_fwd(Q, K, V, log_gamma, r, chunk_size, log_alpha=None, mix_
         raise _lib.HofaError(f"chunk_gla_inlier_fwd: head dim {D} unsupported")
     states_out = torch.empty(B, H, j_pad, d_pad, dtype=torch.float32, device=Q.device)
     state_view = states_out[:, :, :J, :D]
+    if round_operands and chunk_states is not None:
+        raise _lib.HofaError("round_operands is for inference: a backward pass (chunk_states) needs hi/lo operands")
     a, keep = gla_fwd_args(Q, K, V, log_gamma, r, log_alpha, mix_g, gla_scale, Y, state_view, g, eps, chunk_states,
-                           n_out, rstd)
+                           n_out, rstd, round_operands and Q.dtype != torch.float32)
     a.state_pad_rows = j_pad - J
     nbytes = lib.hofa_gla_fwd_workspace_bytes(ctypes.byref(a))
     if nbytes == 0:

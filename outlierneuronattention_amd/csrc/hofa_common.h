@@ -123,6 +123,28 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
+// Lane value moved by a DPP control (GFX9 encoding): lanes whose source is
+// outside the pattern, or whose row is not in ROW_MASK, read 0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_move(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave on the VALU (no LDS
+// round trip): Hillis-Steele inside each row of 16 lanes (row_shr 1, 2, 4,
+// 8; lanes shifted in from outside the row add 0), then row_bcast:15 adds
+// row 0's total to row 1 and row 2's to row 3 (rows 1 and 3 enabled), and
+// row_bcast:31 adds the total of rows 0-1 to rows 2-3.
+__device__ __forceinline__ float wave_incl_scan(float x) {
+    x += dpp_move<0x111>(x);        // row_shr:1
+    x += dpp_move<0x112>(x);        // row_shr:2
+    x += dpp_move<0x114>(x);        // row_shr:4
+    x += dpp_move<0x118>(x);        // row_shr:8
+    x += dpp_move<0x142, 0xa>(x);   // row_bcast:15
+    x += dpp_move<0x143, 0xc>(x);   // row_bcast:31
+    return x;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 constexpr float kLog2e = 1.4426950408889634f;

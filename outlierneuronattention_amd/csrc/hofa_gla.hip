@@ -11,20 +11,23 @@
 //        dS^T[D x J] = V_c^T (K_c (.) exp(G_last - G))        v_mfma_f32_16x16x32
 //      every exponent <= 0.  Writes dS^T and G_last.
 //   2. gla_scan_kernel    grid (B*H, D/16): S_in(c) = S, S <- exp(G_last) S + dS,
-//      writes S_in(c) transposed as a hi/lo pair of 16-bit operands (and, for
-//      a backward pass, untransposed as a second pair) and the final fp32 state.
+//      writes S_in(c) transposed as a hi/lo pair of 16-bit operands (one bf16
+//      plane with round_operands; for a backward pass also untransposed as a
+//      second pair) and the final fp32 state.
 //   3. gla_out_kernel     grid (B*H*nc), 2 waves x 32 query rows:
 //        A^T[key, query] = K~ Q~^T     K~ = K (.) exp(-G), Q~ = Q (.) exp(G)   (masked key <= query)
 //        Y^T[dv, query]  = V_c^T A^T + S_in^T Q~^T                           v_mfma_f32_32x32x16
 //      each lane owns one query row, so the fused epilogue
 //      (1 - mix) * gla_scale * RMSNorm(Y) (src/chunk_gla_inlier.py:130-141)
 //      reduces over D inside a lane pair.  K~ grows like exp(-G); chunks
-//      whose decay range exceeds kSafeRange go to a second launch of the
-//      kernel that forms A^T element-wise from differences G_q - G_k <= 0.
-// Every matrix-core product takes its operands as hi + lo pairs of bf16
-// values (x ~ hi + lo, see split8), i.e. about 16 mantissa bits in the f32
-// exponent range: the result tracks an fp32 computation rather than one
-// rounded to 16-bit operands (f16 inputs use the same bf16 pairs).
+//      whose decay range exceeds kSafeRange form A^T element-wise from
+//      differences G_q - G_k <= 0 in the same launch (a block-uniform branch).
+// By default every matrix-core product takes its operands as hi + lo pairs
+// of bf16 values (x ~ hi + lo, see split8), i.e. about 16 mantissa bits in
+// the f32 exponent range: the result tracks an fp32 computation (f16 inputs
+// use the same bf16 pairs).  With round_operands (16-bit inputs, no backward
+// pass) each operand and the entering state are rounded to bf16 once, as the
+// reference's kernel rounds them, and the state is stored as one bf16 plane.
 #include "hofa_gla_common.h"
 
 namespace hofa {
@@ -34,35 +37,41 @@ using namespace gla;
 constexpr int NT = 128;  // threads of the output kernel
 
 // One block per (head, 16 value rows): thread (dv, j4) carries S[j4..j4+3][dv]
-// in registers across the chunks.  Planes 0/1 (S^T, j contiguous) are stored
-// directly; planes 2/3 (S, d contiguous), written only for a backward pass,
-// go through a double-buffered LDS transpose so that both layouts leave with
-// contiguous stores.
+// in registers across the chunks, with the loads of the next kScanPF chunks
+// in flight.  Plane 0 (and 1) of S^T (j contiguous) are stored directly;
+// planes 2/3 (S, d contiguous), written only for a backward pass, go through
+// a double-buffered LDS transpose so that both layouts leave with contiguous
+// stores.
+constexpr int kScanPF = 8;
+
 template <int DT, int D, int J>
 __global__ __launch_bounds__(kScanRows * J / 4) void gla_scan_kernel(GlaK a) {
     __shared__ __attribute__((aligned(16))) uint16_t sT[2][2][J * kScanPitch];
     const int bh = blockIdx.x, tid = threadIdx.x;
     const int dvl = tid / (J / 4), j4 = (tid % (J / 4)) * 4;
     const int dv0 = blockIdx.y * kScanRows, dv = dv0 + dvl;
+    const int nc = a.nc;
     f32x4 S = {0.f, 0.f, 0.f, 0.f};
-    const int64_t base = (int64_t)bh * a.nc;
-    constexpr int PF = 4;  // chunks whose loads are in flight together
-    for (int c0 = 0; c0 < a.nc; c0 += PF) {
-        f32x4 ds[PF], gl[PF];
+    const int64_t base = (int64_t)bh * nc;
+    f32x4 ds[kScanPF], gl[kScanPF];  // a rolling window: slot u holds chunk c = u (mod kScanPF)
+    auto fetch = [&](int u, int c) {
+        c = min(c, nc - 1);  // past the end: a harmless reload of the last chunk
+        ds[u] = *(const f32x4 *)(a.ws_ds + (base + c) * D * J + dv * J + j4);
+        gl[u] = *(const f32x4 *)(a.ws_gl + (base + c) * J + j4);
+    };
 #pragma unroll
-        for (int u = 0; u < PF; ++u) {
-            const int c = min(c0 + u, a.nc - 1);
-            ds[u] = *(const f32x4 *)(a.ws_ds + (base + c) * D * J + dv * J + j4);
-            gl[u] = *(const f32x4 *)(a.ws_gl + (base + c) * J + j4);
-        }
+    for (int u = 0; u < kScanPF; ++u) fetch(u, u);
+    for (int c0 = 0; c0 < nc; c0 += kScanPF) {
 #pragma unroll
-        for (int u = 0; u < PF; ++u) {
+        for (int u = 0; u < kScanPF; ++u) {
             const int c = c0 + u;
-            if (c >= a.nc) break;  // block-uniform
+            if (c >= nc) break;  // block-uniform
+            const f32x4 d = ds[u], g = gl[u];
+            fetch(u, c + kScanPF);
             store_state_tile<DT, D, J>(a.s_in + (base + c) * a.nplanes * D * J, a.nplanes, dv0, dvl, j4, S,
                                        sT[c & 1][0], sT[c & 1][1]);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) S[e] = fmaf(fast_exp2(gl[u][e] * kLog2e), S[e], ds[u][e]);
+            for (int e = 0; e < 4; ++e) S[e] = fmaf(fast_exp2(g[e] * kLog2e), S[e], d[e]);
         }
     }
     const int b = bh / a.H, h = bh % a.H;
@@ -74,29 +83,31 @@ __global__ __launch_bounds__(kScanRows * J / 4) void gla_scan_kernel(GlaK a) {
         for (int e = 0; e < 4; ++e) so[(J + j4 + e) * a.so_sj + dv * a.so_sd] = 0.f;
 }
 
-// FB = false handles the chunks whose decay range is within kSafeRange with
-// factored operands; FB = true handles the others element-wise.  Both are
-// launched over every chunk and leave at once for the chunks of the other.
-template <int DT, int D, int J, bool GENERAL, bool FB>
+// One block per chunk, 2 waves x 32 query rows.  Every global load of the
+// chunk (decay, V, the wave's Q and K rows, gate inputs) is issued before the
+// first barrier; the entering state is loaded while the decay is prepared.
+// Chunks whose decay range exceeds kSafeRange (a block-uniform test) form
+// A^T element-wise from exponent differences G_q - G_k <= 0 instead of the
+// factored operands.  RND (16-bit inputs): every matrix-core operand is
+// rounded to bf16 once, as the reference's Triton kernel rounds its dot
+// operands (src/chunk_gla_inlier.py:96-110) and the state (S.to(dtype)), and
+// the state comes as one bf16 plane; otherwise operands are hi/lo pairs.
+template <int DT, int D, int J, bool GENERAL, bool RND>
 __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
     using in_t = typename Stor<DT>::type;
     constexpr int VP = C + 4;
     constexpr int MB = D / 32;
     constexpr int KS = J / 16;
-    constexpr bool VLO = kRawSplit<DT>;  // f32/f16 inputs also split V
+    constexpr bool SPLIT = !RND;                   // hi/lo operand pairs
+    constexpr bool VLO = kRawSplit<DT> && SPLIT;   // f32/f16 inputs also split V
+    static_assert(D <= NT, "one gla_scale element per thread");
     __shared__ float sDec[Decay<J, GENERAL>::kFloats];
     __shared__ __attribute__((aligned(16))) uint16_t sVt[VLO ? 2 : 1][D * VP];
     __shared__ __attribute__((aligned(16))) float sGs[D];
-    if ((a.unsafe[blockIdx.x] != 0) != FB) return;  // the other launch handles this chunk
+    constexpr int NSP = SPLIT ? 2 : 1;
+    __shared__ u32x4 sK0[NSP][KS][64];  // wave 0's K~ operand quads, read by wave 1
     const int bh = blockIdx.x / a.nc, c = blockIdx.x % a.nc;
     const int b = bh / a.H, h = bh % a.H, t0 = c * C;
-    const Decay<J, GENERAL> dec{sDec};
-    load_decay<J, GENERAL, NT>(a, b, h, t0, dec);
-    load_transposed<DT, D, VP, VLO, NT>((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, 0, t0, a.T, sVt[0],
-                                    sVt[VLO ? 1 : 0], [](int, int) { return 1.f; });
-    for (int d = threadIdx.x; d < D; d += NT) sGs[d] = a.fuse ? load_any(a.gs, a.gs_dt, h * a.gs_sh + d * a.gs_sd) : 1.f;
-    __syncthreads();
-
     const int lane = threadIdx.x & 63, hi = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int qi = 32 * w + (lane & 31);  // chunk-relative query row of this lane
@@ -105,17 +116,71 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
     const in_t *qp = (const in_t *)a.q + b * a.q_sb + h * a.q_sh;
     const in_t *kp = (const in_t *)a.k + b * a.k_sb + h * a.k_sh;
     const Rows<DT> qrows(qp, a.q_st, a.T), krows(kp, a.k_st, a.T);
-    // 8 inlier channels 16ks + 8hi + e of row t, as floats (0 past T)
-    auto row8 = [&](const Rows<DT> &rows, int t, int ks, float *x) { rows.f8(t, a.R + 16 * ks + 8 * hi, x); };
-    // Q~ = Q (.) exp(G): B operand (lane = query), hi + lo
+    const Rows<DT> vrows((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, a.T);
+
+    // ---- issue every load of the chunk
+    DecayStage<J, GENERAL, NT> dst;
+    TrStage<DT, D, NT> vst;
+    dst.issue(a, b, h, t0);
+    vst.issue(vrows, 0, t0);
+    Raw8<DT> qr[KS], kr[KS];  // this lane's query row and key row (both 32 w + lane%32)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qr[ks].load(qrows, tq, a.R + 16 * ks + 8 * hi);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kr[ks].load(krows, tq, a.R + 16 * ks + 8 * hi);
+    const float mixv =
+        a.fuse && tq < a.T ? load_any(a.mix, a.mix_dt, b * a.m_sb + h * a.m_sh + (int64_t)tq * a.m_st) : 0.f;
+    const float gsv = threadIdx.x < D && a.fuse ? load_any(a.gs, a.gs_dt, h * a.gs_sh + threadIdx.x * a.gs_sd) : 1.f;
+
+    const Decay<J, GENERAL> dec{sDec};
+    dst.commit(a, dec);
+    const bool safe = dec.range() <= kSafeRange;  // block-uniform
+
+    // K~ = K (.) exp(-G) of the wave's own key block (A operand, lane = key);
+    // wave 0 also leaves it in LDS for wave 1, whose queries see both blocks
+    u32x4 kq[NSP][KS];
+    if (safe) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            float x[8];
+            kr[ks].get(x);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(-dec.G(qi, 16 * ks + 8 * hi + e) * kLog2e);
+            if constexpr (SPLIT) split8<OPB>(x, kq[0][ks], kq[NSP - 1][ks]);
+            else kq[0][ks] = pack8<OPB>(x);
+            if (w == 0)
+#pragma unroll
+                for (int p = 0; p < NSP; ++p) sK0[p][ks][lane] = kq[p][ks];
+        }
+    }
+
+    // entering state (chunk 0 starts from zero): A operand rows dv = 32 mb + lane%32
+    u32x4 sst[NSP][MB][KS];
+    if (c > 0) {
+        const uint16_t *sin = a.s_in + ((int64_t)bh * a.nc + c) * a.nplanes * D * J;
+#pragma unroll
+        for (int p = 0; p < NSP; ++p)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    sst[p][mb][ks] = *(const u32x4 *)(sin + p * D * J + (32 * mb + (lane & 31)) * J + 16 * ks + 8 * hi);
+    }
+
+    vst.template commit<VP, VLO>(sVt[0], sVt[VLO ? 1 : 0], [](int, int) { return 1.f; });
+    if (threadIdx.x < D) sGs[threadIdx.x] = gsv;
+    __syncthreads();
+
+    // Q~ = Q (.) exp(G): B operand (lane = query)
     u32x4 qh[KS], ql[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         float x[8];
-        row8(qrows, tq, ks, x);
+        qr[ks].get(x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(dec.G(qi, 16 * ks + 8 * hi + e) * kLog2e);
-        split8<OPB>(x, qh[ks], ql[ks]);
+        if constexpr (SPLIT) split8<OPB>(x, qh[ks], ql[ks]);
+        else qh[ks] = pack8<OPB>(x);
     }
 
     f32x16 y[MB];
@@ -124,26 +189,27 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) y[mb][v] = 0.f;
 
-    for (int kb = 0; kb <= w; ++kb) {  // key blocks at or before the wave's queries
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {  // key blocks at or before the wave's queries
+        if (kb > w) break;
         f32x16 at;
 #pragma unroll
         for (int v = 0; v < 16; ++v) at[v] = 0.f;
-        if constexpr (!FB) {
-            const int kj = 32 * kb + (lane & 31);
+        if (safe) {
+            const bool own = kb == w;  // else wave 1 reading wave 0's block from LDS
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                float x[8];
-                row8(krows, t0 + kj, ks, x);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(-dec.G(kj, 16 * ks + 8 * hi + e) * kLog2e);
-                u32x4 kh, kl;
-                split8<OPB>(x, kh, kl);
+                const u32x4 kh = own ? kq[0][ks] : sK0[0][ks][lane];
                 at = mfma32<OPB>(kh, qh[ks], at);
-                at = mfma32<OPB>(kh, ql[ks], at);
-                at = mfma32<OPB>(kl, qh[ks], at);
+                if constexpr (SPLIT) {
+                    const u32x4 kl = own ? kq[NSP - 1][ks] : sK0[NSP - 1][ks][lane];
+                    at = mfma32<OPB>(kh, ql[ks], at);
+                    at = mfma32<OPB>(kl, qh[ks], at);
+                }
             }
         } else {
             // element-wise: A[q, k] = sum_c q_c k_c exp(G_q,c - G_k,c), every exponent <= 0
+#pragma unroll 1
             for (int ch = 0; ch < J; ++ch) {
                 const float qv = tq < a.T ? to_f32<DT>(qp[(int64_t)tq * a.q_st + a.R + ch]) : 0.f;
                 const float gq = dec.G(qi, ch);
@@ -167,7 +233,8 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2) {
             u32x4 ph, pl;
-            split8v<OPB>(at, 8 * k2, ph, pl);
+            if constexpr (SPLIT) split8v<OPB>(at, 8 * k2, ph, pl);
+            else ph = pack8<OPB>(at, 8 * k2);
             const int ks4 = 2 * kb + k2;
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
@@ -175,7 +242,7 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
                 const uint2 lo = *(const uint2 *)&sVt[0][vo], hi8 = *(const uint2 *)&sVt[0][vo + 8];
                 const u32x4 va = {lo.x, lo.y, hi8.x, hi8.y};
                 y[mb] = mfma32<OPB>(va, ph, y[mb]);
-                y[mb] = mfma32<OPB>(va, pl, y[mb]);
+                if constexpr (SPLIT) y[mb] = mfma32<OPB>(va, pl, y[mb]);
                 if constexpr (VLO) {
                     const uint2 l2 = *(const uint2 *)&sVt[VLO ? 1 : 0][vo],
                                 h2 = *(const uint2 *)&sVt[VLO ? 1 : 0][vo + 8];
@@ -185,16 +252,15 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
         }
     }
     if (c > 0) {  // inter-chunk term: S_in^T Q~^T
-        const uint16_t *sin = a.s_in + ((int64_t)bh * a.nc + c) * a.nplanes * D * J;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
-                const int so = (32 * mb + (lane & 31)) * J + 16 * ks + 8 * hi;
-                const u32x4 sh = *(const u32x4 *)(sin + so), sl = *(const u32x4 *)(sin + D * J + so);
-                y[mb] = mfma32<OPB>(sh, qh[ks], y[mb]);
-                y[mb] = mfma32<OPB>(sh, ql[ks], y[mb]);
-                y[mb] = mfma32<OPB>(sl, qh[ks], y[mb]);
+                y[mb] = mfma32<OPB>(sst[0][mb][ks], qh[ks], y[mb]);
+                if constexpr (SPLIT) {
+                    y[mb] = mfma32<OPB>(sst[0][mb][ks], ql[ks], y[mb]);
+                    y[mb] = mfma32<OPB>(sst[NSP - 1][mb][ks], qh[ks], y[mb]);
+                }
             }
     }
 
@@ -207,8 +273,6 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
             for (int v = 0; v < 16; ++v) ss = fmaf(y[mb][v], y[mb][v], ss);
         ss += __shfl_xor(ss, 32);
         const float rs = rsqrtf(ss / (float)D + a.eps);
-        const float mixv =
-            tq < a.T ? load_any(a.mix, a.mix_dt, b * a.m_sb + h * a.m_sh + (int64_t)tq * a.m_st) : 0.f;
         const float f = (1.f - mixv) * rs;
         if (a.n_out && tq < a.T) {  // RMSNorm(Y_I) and 1/rms, saved for the backward pass
             in_t *nr = (in_t *)a.n_out + b * a.n_sb + h * a.n_sh + (int64_t)tq * a.n_st;
@@ -258,6 +322,13 @@ bool rows_ok(const hofa_view_t &v, int es) {
            (v.stride[1] * es) % 16 == 0 && (v.stride[2] * es) % 16 == 0;
 }
 
+// 16-bit planes per entering state: 4 for a backward pass (chunk_states),
+// one bf16 plane with rounded operands, else a hi/lo pair.
+int state_planes(const hofa_gla_fwd_args_t *a) {
+    if (a->chunk_states) return 4;
+    return a->round_operands && a->q.dtype != HOFA_F32 ? 1 : 2;
+}
+
 struct WsLayout {
     size_t ds, gl, sin, flags, total;
 };
@@ -268,7 +339,7 @@ WsLayout ws_layout(const hofa_gla_fwd_args_t *a) {
     w.ds = 0;
     w.gl = (bh * nc * a->D * J * 4 + 255) / 256 * 256;
     w.sin = w.gl + (bh * nc * J * 4 + 255) / 256 * 256;
-    w.flags = w.sin + (a->chunk_states ? 0 : (bh * nc * 2 * a->D * J * 2 + 255) / 256 * 256);
+    w.flags = w.sin + (a->chunk_states ? 0 : (bh * nc * state_planes(a) * a->D * J * 2 + 255) / 256 * 256);
     w.total = w.flags + (bh * nc + 255) / 256 * 256;
     return w;
 }
@@ -302,31 +373,43 @@ int validate(const hofa_gla_fwd_args_t *a) {
     for (const hofa_view_t *v : {&a->q, &a->k, &a->v})
         HOFA_REQUIRE((int64_t)(a->T + 2 * C) * v->stride[2] * es < (1ll << 31), HOFA_EUNSUPPORTED,
                      "hofa_gla_fwd: one head's q/k/v rows must span less than 2 GiB");
+    HOFA_REQUIRE(!(a->round_operands && a->chunk_states), HOFA_EINVAL,
+                 "hofa_gla_fwd: round_operands is for inference; a backward pass (chunk_states) needs hi/lo operands");
     HOFA_REQUIRE(!a->n_out.data || (a->fuse_norm_gate && a->rstd && a->n_out.dtype == dt && rows_ok(a->n_out, es)),
                  HOFA_EINVAL, "hofa_gla_fwd: n_out needs fuse_norm_gate, rstd, the dtype of y and aligned rows");
     return HOFA_OK;
 }
 
-template <int DT, int D, int J, bool GEN>
+template <int DT, int D, int J, bool GEN, bool RND>
 void launch(const GlaK &k, hipStream_t s) {
     const int nblk = k.B * k.H * k.nc;
-    hipLaunchKernelGGL((gla_state_kernel<DT, D, J, GEN, false>), dim3(nblk), dim3(kStateThreads), 0, s, k);
+    hipLaunchKernelGGL((gla_state_kernel<DT, D, J, GEN, false, RND>), dim3(nblk), dim3(kStateThreads), 0, s, k);
     hipLaunchKernelGGL((gla_scan_kernel<DT, D, J>), dim3(k.B * k.H, D / kScanRows), dim3(kScanRows * J / 4), 0, s, k);
-    hipLaunchKernelGGL((gla_out_kernel<DT, D, J, GEN, false>), dim3(nblk), dim3(NT), 0, s, k);
-    hipLaunchKernelGGL((gla_out_kernel<DT, D, J, GEN, true>), dim3(nblk), dim3(NT), 0, s, k);
+    hipLaunchKernelGGL((gla_out_kernel<DT, D, J, GEN, RND>), dim3(nblk), dim3(NT), 0, s, k);
 }
 
-template <int DT, bool GEN>
+template <int DT, bool GEN, bool RND>
 int dispatch(const GlaK &k, int D, int J, hipStream_t s) {
-    if (D == 64 && J == 48) launch<DT, 64, 48, GEN>(k, s);
-    else if (D == 64 && J == 32) launch<DT, 64, 32, GEN>(k, s);
-    else if (D == 64 && J == 64) launch<DT, 64, 64, GEN>(k, s);
-    else if (D == 128 && J == 112) launch<DT, 128, 112, GEN>(k, s);
-    else if (D == 128 && J == 96) launch<DT, 128, 96, GEN>(k, s);
-    else if (D == 128 && J == 64) launch<DT, 128, 64, GEN>(k, s);
-    else if (D == 128 && J == 128) launch<DT, 128, 128, GEN>(k, s);
+    if (D == 64 && J == 48) launch<DT, 64, 48, GEN, RND>(k, s);
+    else if (D == 64 && J == 32) launch<DT, 64, 32, GEN, RND>(k, s);
+    else if (D == 64 && J == 64) launch<DT, 64, 64, GEN, RND>(k, s);
+    else if (D == 128 && J == 112) launch<DT, 128, 112, GEN, RND>(k, s);
+    else if (D == 128 && J == 96) launch<DT, 128, 96, GEN, RND>(k, s);
+    else if (D == 128 && J == 64) launch<DT, 128, 64, GEN, RND>(k, s);
+    else if (D == 128 && J == 128) launch<DT, 128, 128, GEN, RND>(k, s);
     else return HOFA_EUNSUPPORTED;
     return HOFA_OK;
+}
+
+// f32 inputs always take hi/lo operand pairs.
+template <int DT>
+int dispatch_dt(const GlaK &k, int D, int J, bool gen, bool rnd, hipStream_t s) {
+    if constexpr (DT == HOFA_F32) {
+        return gen ? dispatch<DT, true, false>(k, D, J, s) : dispatch<DT, false, false>(k, D, J, s);
+    } else {
+        if (rnd) return gen ? dispatch<DT, true, true>(k, D, J, s) : dispatch<DT, false, true>(k, D, J, s);
+        return gen ? dispatch<DT, true, false>(k, D, J, s) : dispatch<DT, false, false>(k, D, J, s);
+    }
 }
 
 }  // namespace
@@ -358,7 +441,7 @@ extern "C" int hofa_gla_fwd(const hofa_gla_fwd_args_t *a, void *workspace, size_
     k.ws_ds = (float *)(w + L.ds);
     k.ws_gl = (float *)(w + L.gl);
     k.s_in = a->chunk_states ? (uint16_t *)a->chunk_states : (uint16_t *)(w + L.sin);
-    k.nplanes = a->chunk_states ? 4 : 2;
+    k.nplanes = state_planes(a);
     k.unsafe = (uint8_t *)(w + L.flags);
     k.n_out = (void *)a->n_out.data;
     k.rstd = a->n_out.data ? a->rstd : nullptr;
@@ -385,10 +468,11 @@ extern "C" int hofa_gla_fwd(const hofa_gla_fwd_args_t *a, void *workspace, size_
     const int J = a->D - a->R;
     hipStream_t s = (hipStream_t)stream;
     const bool gen = a->g.data != nullptr;
+    const bool rnd = k.nplanes == 1;
     switch (a->q.dtype) {
-        case HOFA_F32: rc = gen ? dispatch<HOFA_F32, true>(k, a->D, J, s) : dispatch<HOFA_F32, false>(k, a->D, J, s); break;
-        case HOFA_BF16: rc = gen ? dispatch<HOFA_BF16, true>(k, a->D, J, s) : dispatch<HOFA_BF16, false>(k, a->D, J, s); break;
-        default: rc = gen ? dispatch<HOFA_F16, true>(k, a->D, J, s) : dispatch<HOFA_F16, false>(k, a->D, J, s); break;
+        case HOFA_F32: rc = dispatch_dt<HOFA_F32>(k, a->D, J, gen, false, s); break;
+        case HOFA_BF16: rc = dispatch_dt<HOFA_BF16>(k, a->D, J, gen, rnd, s); break;
+        default: rc = dispatch_dt<HOFA_F16>(k, a->D, J, gen, rnd, s); break;
     }
     if (rc) {
         set_error("hofa_gla_fwd: no kernel for this (D, J)");

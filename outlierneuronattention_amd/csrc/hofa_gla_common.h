@@ -100,7 +100,7 @@ struct GlaK {
     float *state_out;
     float *ws_ds;       // [B*H][nc][D][J] f32 per-chunk outer products
     float *ws_gl;       // [B*H][nc][J] f32 per-chunk total log decay
-    uint16_t *s_in;     // [B*H][nc][nplanes][D*J] entering states as 16-bit hi/lo planes
+    uint16_t *s_in;     // [B*H][nc][nplanes][D*J] entering states as 16-bit planes
     uint8_t *unsafe;    // [B*H*nc] per chunk: decay range beyond kSafeRange (set by gla_state_kernel)
     int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, y_sb, y_sh, y_st;
     int64_t n_sb, n_sh, n_st;
@@ -110,7 +110,7 @@ struct GlaK {
     int lg_dt, la_dt, mix_dt, gs_dt;
     int B, H, T, R, nc;
     int key_col0;       // first column of the key operand of gla_state_kernel
-    int nplanes;        // 2: hi/lo of S^T [D][J]; 4: also hi/lo of S [J][D]
+    int nplanes;        // 1: bf16 S^T [D][J]; 2: hi/lo of S^T; 4: also hi/lo of S [J][D]
     int pad_rows;       // state_out rows J .. J+pad_rows-1 to write as zeros
     int fuse;
     int y_f32;          // y is float32 (unrounded result) rather than the input dtype
@@ -154,11 +154,7 @@ __device__ void load_decay(const GlaK &a, int b, int h, int t0, Decay<J, GENERAL
         if (w == 0) {
             const int t = t0 + lane;
             float x = t < a.T ? load_any(a.lg, a.lg_dt, b * a.lg_sb + h * a.lg_sh + (int64_t)t * a.lg_st) : 0.f;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float y = __shfl_up(x, off);
-                if (lane >= off) x += y;
-            }
+            x = wave_incl_scan(x);
             s[lane] = x;
             const float m = wave_max(fabsf(x));
             if (lane == 0) red[0] = m;
@@ -195,15 +191,15 @@ __device__ void load_decay(const GlaK &a, int b, int h, int t0, Decay<J, GENERAL
         if (tid < 4) red[tid] = 0.f;
         __syncthreads();
         float m = 0.f;
-        for (int c = w; c < J; c += NW) {  // one column per wave pass: lane = token
-            float x = s[lane * Decay<J, GENERAL>::GP + c];
+        constexpr int NCOL = (J + NW - 1) / NW;
 #pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float y = __shfl_up(x, off);
-                if (lane >= off) x += y;
+        for (int i = 0; i < NCOL; ++i) {  // columns w, w + NW, ..: lane = token; independent chains
+            const int c = w + i * NW;
+            if (J % NW == 0 || c < J) {
+                const float x = wave_incl_scan(s[lane * Decay<J, GENERAL>::GP + c]);
+                s[lane * Decay<J, GENERAL>::GP + c] = x;
+                m = fmaxf(m, fabsf(x));
             }
-            s[lane * Decay<J, GENERAL>::GP + c] = x;
-            m = fmaxf(m, fabsf(x));
         }
         m = wave_max(m);
         if (lane == 0) red[w] = m;
@@ -240,6 +236,191 @@ __device__ void load_transposed(const typename Stor<DT>::type *base, int64_t row
     }
 }
 
+// ---- two-phase staging: issue() starts a tile's global loads into registers,
+// commit() writes it to LDS later, so that the loads of every tile of a chunk
+// are in flight together instead of one tile per barrier.
+
+// The 16-byte vectors holding 8 consecutive input elements (two for f32).
+template <int DT>
+struct Raw8 {
+    static constexpr int NV = DT == HOFA_F32 ? 2 : 1;
+    u32x4 w[NV];
+    __device__ __forceinline__ void load(const Rows<DT> &rows, int row, int col) {
+        w[0] = bload16(rows.r, rows.off(row, col));
+        if constexpr (NV == 2) w[1] = bload16(rows.r, rows.off(row, col) + 16);
+    }
+    __device__ __forceinline__ void get(float *x) const {
+        if constexpr (NV == 2) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[e] = __uint_as_float(w[0][e]);
+                x[4 + e] = __uint_as_float(w[1][e]);
+            }
+        } else {
+            unpack16<DT>(w[0], x);
+        }
+    }
+};
+
+// A [C x W] chunk tile (columns [col0, col0+W)) in pieces of 2 rows x 8
+// columns per thread, committed to LDS transposed ([W][PITCH] 16-bit
+// operands, tokens contiguous) like load_transposed.
+template <int DT, int W, int NTH>
+struct TrStage {
+    static constexpr int NPIECE = (C / 2) * (W / 8);
+    static constexpr int PT = (NPIECE + NTH - 1) / NTH;
+    Raw8<DT> raw[PT][2];
+    __device__ __forceinline__ void issue(const Rows<DT> &rows, int col0, int t0) {
+#pragma unroll
+        for (int p = 0; p < PT; ++p) {
+            const int pi = threadIdx.x + p * NTH;
+            if (NPIECE % NTH == 0 || pi < NPIECE) {
+                const int tp = pi / (W / 8), cc = pi % (W / 8);
+                raw[p][0].load(rows, t0 + 2 * tp, col0 + 8 * cc);
+                raw[p][1].load(rows, t0 + 2 * tp + 1, col0 + 8 * cc);
+            }
+        }
+    }
+    // Element (t, ch) of the tile is multiplied by scale(t, ch); with LO the
+    // bf16 rounding remainder goes to dst_lo.
+    template <int PITCH, bool LO, typename Scale>
+    __device__ __forceinline__ void commit(uint16_t *dst, uint16_t *dst_lo, Scale scale) const {
+#pragma unroll
+        for (int p = 0; p < PT; ++p) {
+            const int pi = threadIdx.x + p * NTH;
+            if (NPIECE % NTH == 0 || pi < NPIECE) {
+                const int tp = pi / (W / 8), cc = pi % (W / 8);
+                const int t = 2 * tp;
+                float x[2][8];
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    raw[p][r].get(x[r]);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[r][e] *= scale(t + r, 8 * cc + e);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t hv = pack2<OPB>(x[0][e], x[1][e]);
+                    *(uint32_t *)&dst[(8 * cc + e) * PITCH + t] = hv;
+                    if constexpr (LO)
+                        *(uint32_t *)&dst_lo[(8 * cc + e) * PITCH + t] = pack2<OPB>(
+                            x[0][e] - op_to_f32<OPB>(hv & 0xffffu), x[1][e] - op_to_f32<OPB>(hv >> 16));
+                }
+            }
+        }
+    }
+};
+
+// The decay of one chunk: issue() loads it into registers, commit() fills a
+// Decay exactly as load_decay does (ends with a barrier).
+template <int J, bool GENERAL, int NTH>
+struct DecayStage {
+    static_assert(NTH >= 128 && NTH <= 256, "two to four waves");
+    static constexpr int NW = NTH / 64;
+    static constexpr int NG = GENERAL ? (C * J / 4 + NTH - 1) / NTH : 1;
+    static constexpr int NA = (J + 63) / 64;
+    f32x4 gv[NG];  // general: float4 pieces idx = tid + i NTH of the [C][J] tile
+    float lgv;     // scalar decay, wave 0: log_gamma of token t0 + lane
+    float lav[NA]; // scalar decay, wave 1: log_alpha of channel lane + 64 i
+    __device__ __forceinline__ void issue(const GlaK &a, int b, int h, int t0) {
+        const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+        if constexpr (!GENERAL) {
+            if (w == 0) {
+                const int t = t0 + lane;
+                lgv = t < a.T ? load_any(a.lg, a.lg_dt, b * a.lg_sb + h * a.lg_sh + (int64_t)t * a.lg_st) : 0.f;
+            } else if (w == 1) {
+#pragma unroll
+                for (int i = 0; i < NA; ++i) {
+                    const int ch = lane + 64 * i;
+                    lav[i] = a.la && ch < J ? load_any(a.la, a.la_dt, h * a.la_sh + ch * a.la_sj) : 0.f;
+                }
+            }
+        } else {
+            const float *gp = (const float *)a.g + b * a.g_sb + h * a.g_sh;
+            const bool vec = a.g_sj == 1 && (a.g_st % 4) == 0 && (a.g_sb % 4) == 0 && (a.g_sh % 4) == 0 &&
+                             ((uintptr_t)a.g % 16) == 0;
+#pragma unroll
+            for (int i = 0; i < NG; ++i) {
+                const int idx = tid + i * NTH;
+                const int t = idx / (J / 4), c = 4 * (idx % (J / 4));
+                f32x4 x = {0.f, 0.f, 0.f, 0.f};
+                if ((C * J / 4) % NTH == 0 || idx < C * J / 4) {
+                    if (t0 + t < a.T) {
+                        const float *p = gp + (int64_t)(t0 + t) * a.g_st;
+                        if (vec) {
+                            x = *(const f32x4 *)(p + c);
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) x[e] = p[(c + e) * a.g_sj];
+                        }
+                    }
+                }
+                gv[i] = x;
+            }
+        }
+    }
+    __device__ __forceinline__ void commit(const GlaK &a, Decay<J, GENERAL> dec) const {
+        float *s = dec.s, *red = s + Decay<J, GENERAL>::kBody;
+        const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+        if constexpr (!GENERAL) {
+            if (w == 0) {
+                const float x = wave_incl_scan(lgv);
+                s[lane] = x;
+                const float m = wave_max(fabsf(x));
+                if (lane == 0) red[0] = m;
+            } else if (w == 1) {
+                float m = 0.f;
+#pragma unroll
+                for (int i = 0; i < NA; ++i) {
+                    const int ch = lane + 64 * i;
+                    if (ch < J) {
+                        const float al = a.la ? expf(lav[i]) : 1.f;
+                        s[C + ch] = al;
+                        m = fmaxf(m, al);
+                    }
+                }
+                m = wave_max(m);
+                if (lane == 0) red[1] = m;
+            }
+            __syncthreads();
+        } else {
+            constexpr int GP = Decay<J, GENERAL>::GP;
+#pragma unroll
+            for (int i = 0; i < NG; ++i) {
+                const int idx = tid + i * NTH;
+                if ((C * J / 4) % NTH == 0 || idx < C * J / 4) {
+                    const int t = idx / (J / 4), c = 4 * (idx % (J / 4));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) s[t * GP + c + e] = gv[i][e];
+                }
+            }
+            if (tid < 4) red[tid] = 0.f;
+            __syncthreads();
+            float m = 0.f;
+            constexpr int NCOL = (J + NW - 1) / NW;
+            float x[NCOL];
+#pragma unroll
+            for (int i = 0; i < NCOL; ++i) {  // columns w, w + NW, ..: lane = token
+                const int c = w + i * NW;
+                x[i] = J % NW == 0 || c < J ? s[lane * GP + c] : 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < NCOL; ++i) x[i] = wave_incl_scan(x[i]);  // independent chains interleave
+#pragma unroll
+            for (int i = 0; i < NCOL; ++i) {
+                const int c = w + i * NW;
+                if (J % NW == 0 || c < J) {
+                    s[lane * GP + c] = x[i];
+                    m = fmaxf(m, fabsf(x[i]));
+                }
+            }
+            m = wave_max(m);
+            if (lane == 0) red[w] = m;
+            __syncthreads();
+        }
+    }
+};
+
 constexpr int kStateThreads = 256;  // four waves: the LDS footprint allows four blocks per CU
 
 // Per chunk: in-chunk cumsum G of the log decay, then
@@ -248,31 +429,41 @@ constexpr int kStateThreads = 256;  // four waves: the LDS footprint allows four
 // with the key operand read at columns [key_col0, key_col0+J) of a.k and the
 // value operand from a.v (every exponent <= 0).  Writes out^T to ws_ds and
 // G_last to ws_gl, and whether the chunk's decay range exceeds kSafeRange to
-// unsafe[].  4 waves, v_mfma_f32_16x16x32 tiles, hi/lo split operands.
-template <int DT, int D, int J, bool GENERAL, bool BWD>
+// unsafe[].  4 waves, v_mfma_f32_16x16x32 tiles.  The global loads of the
+// decay, key and value tiles are all issued before the first barrier.  RND:
+// the decayed key operand is rounded to bf16 once (the reference's
+// K_c_decayed, src/chunk_gla_inlier.py:118-121); otherwise it is a hi/lo pair.
+template <int DT, int D, int J, bool GENERAL, bool BWD, bool RND = false>
 __global__ __launch_bounds__(kStateThreads) void gla_state_kernel(GlaK a) {
     using in_t = typename Stor<DT>::type;
     constexpr int NTH = kStateThreads;
-    constexpr int TP = C + 8;               // token pitch of the transposed tiles
-    constexpr bool VLO = kRawSplit<DT>;     // f32/f16 inputs also split the value operand
+    constexpr int TP = C + 8;                       // token pitch of the transposed tiles
+    constexpr bool KLO = !RND;                      // key operand as a hi/lo pair
+    constexpr bool VLO = kRawSplit<DT> && !RND;     // f32/f16 inputs also split the value operand
     __shared__ float sDec[Decay<J, GENERAL>::kFloats];
-    __shared__ __attribute__((aligned(16))) uint16_t sKt[2][J * TP];
+    __shared__ __attribute__((aligned(16))) uint16_t sKt[KLO ? 2 : 1][J * TP];
     __shared__ __attribute__((aligned(16))) uint16_t sVt[VLO ? 2 : 1][D * TP];
     const int bh = blockIdx.x / a.nc, c = blockIdx.x % a.nc;
     const int b = bh / a.H, h = bh % a.H, t0 = c * C;
+    const Rows<DT> krows((const in_t *)a.k + b * a.k_sb + h * a.k_sh, a.k_st, a.T);
+    const Rows<DT> vrows((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, a.T);
+    DecayStage<J, GENERAL, NTH> dst;
+    TrStage<DT, J, NTH> kst;
+    TrStage<DT, D, NTH> vst;
+    dst.issue(a, b, h, t0);
+    kst.issue(krows, a.key_col0, t0);
+    vst.issue(vrows, 0, t0);
     const Decay<J, GENERAL> dec{sDec};
-    load_decay<J, GENERAL, NTH>(a, b, h, t0, dec);
+    dst.commit(a, dec);
     if (threadIdx.x == 0) a.unsafe[blockIdx.x] = dec.range() > kSafeRange;
-    const in_t *kb = (const in_t *)a.k + b * a.k_sb + h * a.k_sh;
     if constexpr (BWD)
-        load_transposed<DT, J, TP, true, NTH>(kb, a.k_st, a.key_col0, t0, a.T, sKt[0], sKt[1],
-                                              [&](int t, int ch) { return fast_exp2(dec.G(t, ch) * kLog2e); });
+        kst.template commit<TP, KLO>(sKt[0], sKt[KLO ? 1 : 0],
+                                     [&](int t, int ch) { return fast_exp2(dec.G(t, ch) * kLog2e); });
     else
-        load_transposed<DT, J, TP, true, NTH>(kb, a.k_st, a.key_col0, t0, a.T, sKt[0], sKt[1], [&](int t, int ch) {
+        kst.template commit<TP, KLO>(sKt[0], sKt[KLO ? 1 : 0], [&](int t, int ch) {
             return fast_exp2((dec.last(ch) - dec.G(t, ch)) * kLog2e);
         });
-    load_transposed<DT, D, TP, VLO, NTH>((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, 0, t0, a.T, sVt[0],
-                                         sVt[VLO ? 1 : 0], [](int, int) { return 1.f; });
+    vst.template commit<TP, VLO>(sVt[0], sVt[VLO ? 1 : 0], [](int, int) { return 1.f; });
     __syncthreads();
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int r16 = lane & 15, g4 = lane >> 4;
@@ -287,7 +478,7 @@ __global__ __launch_bounds__(kStateThreads) void gla_state_kernel(GlaK a) {
             const int ko = (16 * tn + r16) * TP + 32 * ks + 8 * g4;
             const u32x4 av = *(const u32x4 *)&sVt[0][vo];
             acc = mfma16<OPB>(av, *(const u32x4 *)&sKt[0][ko], acc);
-            acc = mfma16<OPB>(av, *(const u32x4 *)&sKt[1][ko], acc);
+            if constexpr (KLO) acc = mfma16<OPB>(av, *(const u32x4 *)&sKt[KLO ? 1 : 0][ko], acc);
             if constexpr (VLO) acc = mfma16<OPB>(*(const u32x4 *)&sVt[VLO ? 1 : 0][vo], *(const u32x4 *)&sKt[0][ko], acc);
         }
 #pragma unroll
@@ -303,24 +494,14 @@ __device__ __forceinline__ void split4(const f32x4 &s, uint2 &hv, uint2 &lv) {
                pack2<OPB>(s[2] - op_to_f32<OPB>(hv.y & 0xffffu), s[3] - op_to_f32<OPB>(hv.y >> 16))};
 }
 
-// Store the state elements (dv, j4..j4+3) of one chunk as bf16 hi/lo planes:
-// planes 0/1 hold S^T ([D][J], j contiguous); with four planes, planes 2/3
-// hold S ([J][D], d contiguous).
-template <int DT, int D, int J>
-__device__ __forceinline__ void store_state_planes(uint16_t *dst, int nplanes, int dv, int j4, const f32x4 &S) {
+// Store the state elements (dv, j4..j4+3) of S^T ([D][J], j contiguous) as
+// plane 0 (bf16 rounding) and, with two or more planes, plane 1 (remainder).
+__device__ __forceinline__ void store_state_planes(uint16_t *dst, int nplanes, int D, int J, int dv, int j4,
+                                                   const f32x4 &S) {
     uint2 hv, lv;
     split4(S, hv, lv);
     *(uint2 *)(dst + dv * J + j4) = hv;
-    *(uint2 *)(dst + D * J + dv * J + j4) = lv;
-    if (nplanes == 4) {
-        uint16_t *p2 = dst + 2 * D * J, *p3 = dst + 3 * D * J;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t hb = e < 2 ? hv.x : hv.y, lb = e < 2 ? lv.x : lv.y;
-            p2[(j4 + e) * D + dv] = (uint16_t)((e & 1) ? hb >> 16 : hb & 0xffffu);
-            p3[(j4 + e) * D + dv] = (uint16_t)((e & 1) ? lb >> 16 : lb & 0xffffu);
-        }
-    }
+    if (nplanes >= 2) *(uint2 *)(dst + D * J + dv * J + j4) = lv;
 }
 
 // The scans run one block per (head, kScanRows value rows) with thread
@@ -328,15 +509,15 @@ __device__ __forceinline__ void store_state_planes(uint16_t *dst, int nplanes, i
 constexpr int kScanRows = 16;
 constexpr int kScanPitch = kScanRows + 4;  // LDS row pitch: 8-byte aligned rows, spread banks
 
-// Store one chunk's state from a scan block: planes 0/1 (S^T) directly; with
-// four planes, planes 2/3 (S, d contiguous) through the LDS tile
+// Store one chunk's state from a scan block: planes 0 (and 1) of S^T
+// directly; with four planes, planes 2/3 (S, d contiguous) through the LDS tile
 // sT[2][J * kScanPitch] (hi, lo), so that they also leave with contiguous
 // stores.  Contains a barrier when nplanes == 4 (block-uniform); callers
 // alternate between two tiles, so one barrier per chunk suffices.
 template <int DT, int D, int J>
 __device__ __forceinline__ void store_state_tile(uint16_t *dst, int nplanes, int dv0, int dvl, int j4,
                                                  const f32x4 &S, uint16_t *th, uint16_t *tl) {
-    store_state_planes<DT, D, J>(dst, 2, dv0 + dvl, j4, S);
+    store_state_planes(dst, nplanes, D, J, dv0 + dvl, j4, S);
     if (nplanes != 4) return;
     uint2 hv, lv;
     split4(S, hv, lv);

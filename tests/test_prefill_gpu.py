@@ -107,29 +107,39 @@ GLA_CASES = [
 ]
 
 
-def _check_gla(B, H, T, D, R, dtype, mode, strength=1.0, seed=0):
+def _check_gla(B, H, T, D, R, dtype, mode, strength=1.0, seed=0, round_operands=False):
+    """round_operands: operands and state rounded to bf16 once (16-bit inputs),
+    as the reference kernel does; else hi/lo operand pairs (the default)."""
     from outlierneuronattention_amd.chunk_gla_inlier import chunk_gla_inlier_fwd
     q, k, v, lg, la, g, mix, gs = _gla_inputs(B, H, T, D, R, dtype, mode, seed, strength)
     J = D - R
-    kw = dict(log_alpha=None if la is None else la.to(DEV), mix_g=mix.to(DEV, dtype), gla_scale=gs.to(DEV))
+    kw = dict(log_alpha=None if la is None else la.to(DEV), mix_g=mix.to(DEV, dtype), gla_scale=gs.to(DEV),
+              round_operands=round_operands)
     if g is not None:
         kw["g"] = g.to(DEV)
     Y, states = chunk_gla_inlier_fwd(q, k, v, lg.to(DEV), R, 64, **kw)
-    Yraw, _ = chunk_gla_inlier_fwd(q, k, v, lg.to(DEV), R, 64, log_alpha=kw["log_alpha"], g=kw.get("g"))
+    Yraw, _ = chunk_gla_inlier_fwd(q, k, v, lg.to(DEV), R, 64, log_alpha=kw["log_alpha"], g=kw.get("g"),
+                                   round_operands=round_operands)
     torch.cuda.synchronize()
     gd = g.double() if g is not None else ref.decay_from_gates(lg.double(), J, None if la is None else la.double())
     y_i, S = ref.gla_chunked(_c(q)[..., R:], _c(k)[..., R:], _c(v), gd, chunk=64)
     y_fused = (1 - _c(kw["mix_g"])) * gs.double() * ref.rmsnorm(y_i, 1e-5)
-    tol = 3e-2 if dtype == torch.float32 else 2e-2
+    rounded = dtype != torch.float32 and round_operands
+    # hi/lo operands track fp32: the state within 1e-3, outputs within the bf16 bar.  Operands
+    # rounded to bf16 once (the reference's .to(dtype) before each tl.dot) leave ~2^-9 relative per
+    # product term, which RMSNorm magnifies on tokens of small norm.
+    tol = 3e-2 if dtype == torch.float32 else (6e-2 if rounded else 2e-2)
+    state_tol = 6e-3 if rounded else 1e-3
     scale = max(1.0, y_i.abs().max().item())
     err_raw = ((_c(Yraw) - y_i).abs().max() / scale).item()
-    assert err_raw <= tol, f"raw Y_I rel-max err {err_raw}"
     err = (_c(Y) - y_fused).abs().max().item()
-    assert err <= tol, f"fused Y err {err}"
-    assert states.shape == (B, H, max(16, 1 << (J - 1).bit_length()), max(16, 1 << (D - 1).bit_length()))
     s = states[:, :, :J, :D].cpu().double()
     rel = ((s - S).norm() / S.norm()).item()
-    assert rel <= 1e-3, f"state rel err {rel}"
+    print(f"  rounded={rounded}: raw rel-max {err_raw:.3e}, fused max-abs {err:.3e}, state rel {rel:.3e}", flush=True)
+    assert err_raw <= tol, f"raw Y_I rel-max err {err_raw}"
+    assert err <= tol, f"fused Y err {err}"
+    assert states.shape == (B, H, max(16, 1 << (J - 1).bit_length()), max(16, 1 << (D - 1).bit_length()))
+    assert rel <= state_tol, f"state rel err {rel}"
     assert torch.count_nonzero(states[:, :, J:, :]) == 0
 
 
@@ -137,6 +147,14 @@ def _check_gla(B, H, T, D, R, dtype, mode, strength=1.0, seed=0):
 def test_chunk_gla_matches_oracle(B, H, T, D, R, dtype, mode):
     print(f"gla B={B} H={H} T={T} D={D} R={R} {dtype} {mode}", flush=True)
     _check_gla(B, H, T, D, R, dtype, mode)
+
+
+@pytest.mark.parametrize("B,H,T,D,R,dtype,mode", [c for c in GLA_CASES if c[5] != torch.float32][:3] +
+                         [(1, 2, 200, 128, 16, torch.bfloat16, "alpha"), (1, 2, 190, 64, 16, torch.float16, "alpha")])
+def test_chunk_gla_rounded_operands(B, H, T, D, R, dtype, mode):
+    """round_operands=True: operands rounded to bf16 once, the reference kernel's numerics."""
+    print(f"gla rounded B={B} H={H} T={T} D={D} R={R} {dtype} {mode}", flush=True)
+    _check_gla(B, H, T, D, R, dtype, mode, round_operands=True)
 
 
 @pytest.mark.parametrize("mode", ["scalar", "alpha", "general"])
