@@ -39,6 +39,7 @@
 // parallel; hofa_gla_bwd.hip holds the C entry point.
 #pragma once
 #include "hofa_gla_common.h"
+#include "hofa_tile.h"
 
 namespace hofa {
 namespace glabwd {
@@ -225,9 +226,30 @@ __global__ __launch_bounds__(kScanRows * J / 4) void gla_bwd_scan_kernel(GlaBwdK
 // FB = false: chunks whose decay range is within kSafeRange (factored
 // operands); FB = true: the others (element-wise intra-chunk terms).  Both
 // are launched over every chunk and leave at once for the chunks of the other.
+//
+// Every global load a block needs is issued before its first barrier: the
+// decay, the three transposed operand tiles (Q~^T, K~^T, dO^T), each side's
+// own rows and the rows of its first loop iteration; a wave whose loop runs
+// twice fetches the second iteration's rows during the first.  For D = 64 the
+// [J][D] hi/lo planes of the exiting (key side) and entering (query side)
+// states go to LDS by DMA in the same phase; the key side reads S_end^T as a
+// transposing read of the same tiles.
+template <int DT>
+__device__ __forceinline__ void raw_op(const Raw8<DT> &r, u32x4 &hi, u32x4 &lo) {
+    if constexpr (DT == HOFA_BF16) {
+        hi = r.w[0];
+        lo = u32x4{0, 0, 0, 0};
+    } else {
+        float x[8];
+        r.get(x);
+        split8<OPB>(x, hi, lo);
+    }
+}
+
 template <int DT, int D, int J, bool GENERAL, bool FB>
 __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
     using in_t = typename Stor<DT>::type;
+    using tile::TileL;
     constexpr int TP = C + 4;             // token pitch of the transposed tiles
     constexpr int JB = (J + 31) / 32;     // 32-row channel blocks
     constexpr int JP = 32 * JB;
@@ -237,26 +259,80 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
     constexpr bool SPL = kRawSplit<DT>;   // raw f32/f16 inputs are split as well
     constexpr int NO = SPL ? 2 : 1;
     constexpr int DGP = J + 1;             // pitch of the dGamma tile
+    constexpr bool SLDS = D == 64 && J <= 64;  // state planes staged in LDS (one 64-row tile each)
+    static_assert(NTB == tile::NT, "the state DMA splits each tile over four waves");
     __shared__ float sDec[Decay<J, GENERAL>::kFloats];
     __shared__ __attribute__((aligned(16))) uint16_t sQK[2][2][JP * TP];  // [Q~^T | K~^T][hi | lo]
     __shared__ __attribute__((aligned(16))) uint16_t sOt[NO][D * TP];     // dO^T
+    // [S_end hi, S_end lo, S_in hi, S_in lo], each [J][D] in the TileL<64> layout
+    __shared__ __attribute__((aligned(16))) uint16_t sSt[SLDS ? 4 : 1][SLDS ? TileL<64>::ELEMS : 8];
     static_assert(sizeof(sQK) >= sizeof(float) * C * DGP, "dGamma reuses the operand tiles");
+    static_assert(sizeof(sOt) >= sizeof(float) * 2 * NTB, "the channel sums reuse the dO tile");
 
     const int nc = a.f.nc, H = a.f.H, T = a.f.T, R = a.f.R;
     const int bh = blockIdx.x / nc, c = blockIdx.x % nc;
     const int b = bh / H, h = bh % H, t0 = c * C;
     if ((a.f.unsafe[blockIdx.x] != 0) != FB) return;  // the other launch handles this chunk
-    const Decay<J, GENERAL> dec{sDec};
-    load_decay<J, GENERAL, NTB>(a.f, b, h, t0, dec);
+    constexpr bool safe = !FB;
     const in_t *qp = (const in_t *)a.f.q + b * a.f.q_sb + h * a.f.q_sh;
     const in_t *kp = (const in_t *)a.f.k + b * a.f.k_sb + h * a.f.k_sh;
     const in_t *vp = (const in_t *)a.f.v + b * a.f.v_sb + h * a.f.v_sh;
     const in_t *dop = (const in_t *)a.ws_do + (int64_t)bh * T * D;
-    load_transposed<DT, J, TP, true, NTB>(qp, a.f.q_st, R, t0, T, sQK[0][0], sQK[0][1],
-                                          [&](int t, int ch) { return fast_exp2(dec.G(t, ch) * kLog2e); });
-    load_transposed<DT, J, TP, true, NTB>(kp, a.f.k_st, R, t0, T, sQK[1][0], sQK[1][1],
-                                          [&](int t, int ch) { return fast_exp2(-dec.G(t, ch) * kLog2e); });
-    load_transposed<DT, D, TP, SPL, NTB>(dop, D, 0, t0, T, sOt[0], sOt[NO - 1], [](int, int) { return 1.f; });
+    const Rows<DT> qrows(qp, a.f.q_st, T), krows(kp, a.f.k_st, T), vrows(vp, a.f.v_st, T), drows(dop, D, T);
+    const int lane = threadIdx.x & 63, hi = lane >> 5, l32 = lane & 31;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool keyside = w < 2;
+    const int own = 32 * (w & 1) + l32;  // key side: key s; query side: query t (chunk-relative)
+    const uint16_t *sin = a.s_in + ((int64_t)bh * nc + c) * 4 * D * J;
+    const uint16_t *dse = a.ds_end + ((int64_t)bh * nc + c) * 4 * D * J;
+
+    // ---- issue the loads
+    DecayStage<J, GENERAL, NTB> dstage;
+    TrStage<DT, J, NTB> qst, kst;
+    TrStage<DT, D, NTB> ost;
+    dstage.issue(a.f, b, h, t0);
+    qst.issue(qrows, R, t0);
+    kst.issue(krows, R, t0);
+    ost.issue(drows, 0, t0);
+    Raw8<DT> rA[DKS];  // key side: V row of key own; query side: dO row of query own
+    Raw8<DT> rK[KS];   // key side: K row of key own
+    Raw8<DT> iA[DKS];  // rows of the current iteration: key side dO, query side V
+    Raw8<DT> iQ[KS];   // key side: Q rows of the current iteration
+    if (keyside) {
+#pragma unroll
+        for (int ks = 0; ks < DKS; ++ks) rA[ks].load(vrows, t0 + own, 16 * ks + 8 * hi);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) rK[ks].load(krows, t0 + own, R + 16 * ks + 8 * hi);
+#pragma unroll
+        for (int ks = 0; ks < DKS; ++ks) iA[ks].load(drows, t0 + own, 16 * ks + 8 * hi);  // first tb = kb
+        if constexpr (safe) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) iQ[ks].load(qrows, t0 + own, R + 16 * ks + 8 * hi);
+        }
+    } else {
+#pragma unroll
+        for (int ks = 0; ks < DKS; ++ks) rA[ks].load(drows, t0 + own, 16 * ks + 8 * hi);
+#pragma unroll
+        for (int ks = 0; ks < DKS; ++ks) iA[ks].load(vrows, t0 + l32, 16 * ks + 8 * hi);  // first sb = 0
+    }
+    if constexpr (SLDS) {  // issued last: waiting for the loads above does not wait for these
+        tile::TileDma<64> dm;
+        const uint16_t *src[4] = {dse + 2 * D * J, dse + 3 * D * J, sin + 2 * D * J, sin + 3 * D * J};
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            dm.init(src[p], D, J, w, lane);
+            dm.fetch(sSt[p], 0, w);
+        }
+    }
+
+    // ---- decay, then the transposed operand tiles
+    const Decay<J, GENERAL> dec{sDec};
+    dstage.commit(a.f, dec);
+    qst.template commit<TP, true>(sQK[0][0], sQK[0][1],
+                                  [&](int t, int ch) { return fast_exp2(dec.G(t, ch) * kLog2e); });
+    kst.template commit<TP, true>(sQK[1][0], sQK[1][1],
+                                  [&](int t, int ch) { return fast_exp2(-dec.G(t, ch) * kLog2e); });
+    ost.template commit<TP, SPL>(sOt[0], sOt[NO - 1], [](int, int) { return 1.f; });
     if constexpr (JP > J) {
         for (int i = threadIdx.x; i < (JP - J) * TP; i += NTB) {
             sQK[0][0][J * TP + i] = 0;
@@ -267,18 +343,23 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
     }
     __syncthreads();
 
-    const int lane = threadIdx.x & 63, hi = lane >> 5, l32 = lane & 31;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    constexpr bool safe = !FB;
-    const uint16_t *sin = a.s_in + ((int64_t)bh * nc + c) * 4 * D * J;
-    const uint16_t *dse = a.ds_end + ((int64_t)bh * nc + c) * 4 * D * J;
     auto qval = [&](int ti, int ch) { return t0 + ti < T ? to_f32<DT>(qp[(int64_t)(t0 + ti) * a.f.q_st + R + ch]) : 0.f; };
     auto kval = [&](int ti, int ch) { return t0 + ti < T ? to_f32<DT>(kp[(int64_t)(t0 + ti) * a.f.k_st + R + ch]) : 0.f; };
     const u32x4 zero4 = {0, 0, 0, 0};
-    const Rows<DT> qrows(qp, a.f.q_st, T), krows(kp, a.f.k_st, T), vrows(vp, a.f.v_st, T), drows(dop, D, T);
     // K~ / Q~ (= k e^-G / q e^G) at (channel, chunk token) from the staged operands
     auto staged = [&](int which, int ch, int tk) {
         return op_to_f32<OPB>(sQK[which][0][ch * TP + tk]) + op_to_f32<OPB>(sQK[which][1][ch * TP + tk]);
+    };
+    // S rows (channel cr, 8 value columns from col) of a [J][D] state plane pair
+    auto state_row = [&](int which, const uint16_t *g2, int cr, int col, u32x4 &sh, u32x4 &sl) {
+        if constexpr (SLDS) {
+            const int o = TileL<64>::off(cr, col);
+            sh = *(const u32x4 *)&sSt[2 * which][o];
+            sl = *(const u32x4 *)&sSt[2 * which + 1][o];
+        } else {
+            sh = cr < J ? *(const u32x4 *)(g2 + cr * D + col) : zero4;
+            sl = cr < J ? *(const u32x4 *)(g2 + D * J + cr * D + col) : zero4;
+        }
     };
 
     f32x16 acc[JB];  // dk^T (key side) or dq^T (query side): rows = channel, col = token
@@ -286,12 +367,11 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
     for (int jb = 0; jb < JB; ++jb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[jb][v] = 0.f;
-    int tok;  // chunk-relative token of this lane's column
+    const int tok = own;  // chunk-relative token of this lane's column
 
-    if (w < 2) {
+    if (keyside) {
         // ================= key side: keys s = 32w + l32
-        const int kb = w, s = 32 * kb + l32, ts = t0 + s;
-        tok = s;
+        const int kb = w, s = own, ts = t0 + s;
         f32x16 dvt[MB];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
@@ -299,21 +379,30 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
             for (int v = 0; v < 16; ++v) dvt[mb][v] = 0.f;
         u32x4 vh[DKS], vl[DKS];
 #pragma unroll
-        for (int ks = 0; ks < DKS; ++ks) {
-            vrows.op8(ts, 16 * ks + 8 * hi, vh[ks], vl[ks]);
-        }
+        for (int ks = 0; ks < DKS; ++ks) raw_op<DT>(rA[ks], vh[ks], vl[ks]);
         u32x4 kth[KS], ktl[KS];  // K~ = k e^-G of this key
         if constexpr (safe) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 float x[8];
-                krows.f8(ts, R + 16 * ks + 8 * hi, x);
+                rK[ks].get(x);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(-dec.G(s, 16 * ks + 8 * hi + e) * kLog2e);
                 split8<OPB>(x, kth[ks], ktl[ks]);
             }
         }
-        for (int tb = kb; tb < 2; ++tb) {
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            if (tb < kb) continue;
+            Raw8<DT> nA[DKS], nQ[KS];
+            if (tb == 0) {  // wave 0 also has tb = 1: fetch its rows now
+#pragma unroll
+                for (int ks = 0; ks < DKS; ++ks) nA[ks].load(drows, t0 + 32 + l32, 16 * ks + 8 * hi);
+                if constexpr (safe) {
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) nQ[ks].load(qrows, t0 + 32 + l32, R + 16 * ks + 8 * hi);
+                }
+            }
             const int tr = 32 * tb + l32;  // A-operand row (query) of this lane
             f32x16 mt, at;
 #pragma unroll
@@ -325,7 +414,7 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
             for (int ks = 0; ks < DKS; ++ks) {
                 u32x4 oh, ol;
-                drows.op8(t0 + tr, 16 * ks + 8 * hi, oh, ol);
+                raw_op<DT>(iA[ks], oh, ol);
                 mt = mfma32<OPB>(oh, vh[ks], mt);
                 if constexpr (SPL) {
                     mt = mfma32<OPB>(oh, vl[ks], mt);
@@ -337,7 +426,7 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
                     float x[8];
-                    qrows.f8(t0 + tr, R + 16 * ks + 8 * hi, x);
+                    iQ[ks].get(x);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) x[e] *= fast_exp2(dec.G(tr, 16 * ks + 8 * hi + e) * kLog2e);
                     u32x4 qh, ql;
@@ -409,7 +498,15 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
                         acc[jb][vv] += x;
                     }
             }
+            if (tb == 0) {
+#pragma unroll
+                for (int ks = 0; ks < DKS; ++ks) iA[ks] = nA[ks];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) iQ[ks] = nQ[ks];
+            }
         }
+        if constexpr (SLDS) tile::wait_vmem();
+        __syncthreads();  // the state tiles are complete (the query side waits at its own barrier)
         in_t *dkr = (in_t *)a.dk + b * a.dk_sb + h * a.dk_sh + (int64_t)ts * a.dk_st + R;
         in_t *dvr = (in_t *)a.dv + b * a.dv_sb + h * a.dv_sh + (int64_t)ts * a.dv_st;
         // dk = e^-G (intra + e^G_last X) (factored) or intra + e^(G_last - G) X (element-wise),
@@ -421,9 +518,8 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
             if (c < nc - 1) {
 #pragma unroll
                 for (int ks = 0; ks < DKS; ++ks) {
-                    const int off = cr * D + 16 * ks + 8 * hi;
-                    const u32x4 sh = cr < J ? *(const u32x4 *)(dse + 2 * D * J + off) : zero4;
-                    const u32x4 sl = cr < J ? *(const u32x4 *)(dse + 3 * D * J + off) : zero4;
+                    u32x4 sh, sl;
+                    state_row(0, dse + 2 * D * J, cr, 16 * ks + 8 * hi, sh, sl);
                     x = mfma32<OPB>(sh, vh[ks], x);
                     x = mfma32<OPB>(sl, vh[ks], x);
                     if constexpr (SPL) x = mfma32<OPB>(sh, vl[ks], x);
@@ -457,7 +553,7 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 float x[8];
-                krows.f8(ts, R + 16 * ks + 8 * hi, x);
+                rK[ks].get(x);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int ch = 16 * ks + 8 * hi + e;
@@ -467,8 +563,15 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
                 split8<OPB>(x, kh, kl);
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb) {
-                    const int off = (32 * mb + l32) * J + 16 * ks + 8 * hi;
-                    const u32x4 sh = *(const u32x4 *)(dse + off), sl = *(const u32x4 *)(dse + D * J + off);
+                    u32x4 sh, sl;
+                    if constexpr (SLDS) {  // A[d, c] = S_end[c][d]: transposing reads of the state tiles
+                        sh = tile::tr_operand_lin<64>(sSt[0], 16 * ks, 32 * mb, lane);
+                        sl = tile::tr_operand_lin<64>(sSt[1], 16 * ks, 32 * mb, lane);
+                    } else {
+                        const int off = (32 * mb + l32) * J + 16 * ks + 8 * hi;
+                        sh = *(const u32x4 *)(dse + off);
+                        sl = *(const u32x4 *)(dse + D * J + off);
+                    }
                     dvt[mb] = mfma32<OPB>(sh, kh, dvt[mb]);
                     dvt[mb] = mfma32<OPB>(sh, kl, dvt[mb]);
                     dvt[mb] = mfma32<OPB>(sl, kh, dvt[mb]);
@@ -485,15 +588,18 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
         }
     } else {
         // ================= query side: queries t = 32(w-2) + l32
-        const int qb = w - 2, t = 32 * qb + l32, tq = t0 + t;
-        tok = t;
+        const int qb = w - 2, t = own, tq = t0 + t;
         u32x4 dh[DKS], dl[DKS];
 #pragma unroll
-        for (int ks = 0; ks < DKS; ++ks) {
-            drows.op8(tq, 16 * ks + 8 * hi, dh[ks], dl[ks]);
-        }
-        for (int sb = 0; sb <= qb; ++sb) {
-            const int sr = 32 * sb + l32;  // A-operand row (key) of this lane
+        for (int ks = 0; ks < DKS; ++ks) raw_op<DT>(rA[ks], dh[ks], dl[ks]);
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            if (sb > qb) break;
+            Raw8<DT> nA[DKS];
+            if (sb == 0 && qb == 1) {  // fetch the second key block's rows now
+#pragma unroll
+                for (int ks = 0; ks < DKS; ++ks) nA[ks].load(vrows, t0 + 32 + l32, 16 * ks + 8 * hi);
+            }
             f32x16 mt;
 #pragma unroll
             for (int v = 0; v < 16; ++v) mt[v] = 0.f;
@@ -501,7 +607,7 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
             for (int ks = 0; ks < DKS; ++ks) {
                 u32x4 va, vla;
-                vrows.op8(t0 + sr, 16 * ks + 8 * hi, va, vla);
+                raw_op<DT>(iA[ks], va, vla);
                 mt = mfma32<OPB>(va, dh[ks], mt);
                 if constexpr (SPL) {
                     mt = mfma32<OPB>(va, dl[ks], mt);
@@ -546,7 +652,13 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
                         acc[jb][vv] += x;
                     }
             }
+            if (sb == 0 && qb == 1) {
+#pragma unroll
+                for (int ks = 0; ks < DKS; ++ks) iA[ks] = nA[ks];
+            }
         }
+        if constexpr (SLDS) tile::wait_vmem();
+        __syncthreads();  // pairs with the key side's barrier: the state tiles are complete
         // dq^T[c, t] (+)= e^G_tc (sum_d S_in[c, d] dO[t, d])
 #pragma unroll
         for (int jb = 0; jb < JB; ++jb) {
@@ -557,9 +669,8 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
             if (c > 0) {
 #pragma unroll
                 for (int ks = 0; ks < DKS; ++ks) {
-                    const int off = cr * D + 16 * ks + 8 * hi;
-                    const u32x4 sh = cr < J ? *(const u32x4 *)(sin + 2 * D * J + off) : zero4;
-                    const u32x4 sl = cr < J ? *(const u32x4 *)(sin + 3 * D * J + off) : zero4;
+                    u32x4 sh, sl;
+                    state_row(1, sin + 2 * D * J, cr, 16 * ks + 8 * hi, sh, sl);
                     x = mfma32<OPB>(sh, dh[ks], x);
                     x = mfma32<OPB>(sl, dh[ks], x);
                     if constexpr (SPL) x = mfma32<OPB>(sh, dl[ks], x);
@@ -619,41 +730,60 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
     }
     __syncthreads();
     float *cp = a.chunk_part + ((int64_t)bh * nc + c) * (2 * J + 2);
+    const int tid = threadIdx.x;
     if constexpr (!GENERAL) {
         const float *sLam = sDec, *sAl = sDec + C;
-        if (w == 0) {
+        if (w == 0) {  // d log_gamma partial: suffix over the chunk's tokens of sum_c alpha_c dGamma
             float e = 0.f;
             for (int ch = 0; ch < J; ++ch) e = fmaf(sAl[ch], sDG[lane * DGP + ch], e);
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float y = __shfl_down(e, off);
-                if (lane + off < 64) e += y;
-            }
-            if (t0 + lane < T) a.dlg_part[(int64_t)bh * T + t0 + lane] = e;
+            const float incl = wave_incl_scan(e);
+            const float total = __shfl(incl, 63);
+            if (t0 + lane < T) a.dlg_part[(int64_t)bh * T + t0 + lane] = total - incl + e;
             if (lane == 0) {
-                cp[2 * J] = e;
+                cp[2 * J] = total;
                 cp[2 * J + 1] = sLam[C - 1];
             }
         }
-        for (int ch = threadIdx.x; ch < J; ch += NTB) {
-            float ed = 0.f, f = 0.f;
-            for (int t = 0; t < C; ++t) {
+        // per channel: sum_t dGamma and sum_t dGamma Lambda_t, NSEG token segments per channel
+        constexpr int NSEG = NTB / J;
+        float *red = (float *)&sOt[0][0];
+        const int ch = tid % J, seg = tid / J;
+        float ed = 0.f, f = 0.f;
+        if (seg < NSEG) {
+            for (int t = seg; t < C; t += NSEG) {
                 const float x = sDG[t * DGP + ch];
                 ed += x;
                 f = fmaf(x, sLam[t], f);
             }
-            cp[ch] = ed;
-            cp[J + ch] = f;
+        }
+        red[tid] = ed;
+        red[NTB + tid] = f;
+        __syncthreads();
+        if (tid < J) {
+            float se = 0.f, sf = 0.f;
+#pragma unroll
+            for (int sg = 0; sg < NSEG; ++sg) {
+                se += red[sg * J + tid];
+                sf += red[NTB + sg * J + tid];
+            }
+            cp[tid] = se;
+            cp[J + tid] = sf;
         }
     } else {
+        // d g: suffix over the chunk's tokens per channel (lane = token), written back, then stored by rows
+        constexpr int NW = NTB / 64;
+        for (int ch = w; ch < J; ch += NW) {
+            const float x = sDG[lane * DGP + ch];
+            const float incl = wave_incl_scan(x);
+            const float total = __shfl(incl, 63);
+            sDG[lane * DGP + ch] = total - incl + x;
+            if (lane == 0) cp[ch] = total;
+        }
+        __syncthreads();
         float *dg = (float *)a.dg + b * a.dg_sb + h * a.dg_sh;
-        for (int ch = threadIdx.x; ch < J; ch += NTB) {
-            float s = 0.f;
-            for (int t = C - 1; t >= 0; --t) {
-                s += sDG[t * DGP + ch];
-                if (t0 + t < T) dg[(int64_t)(t0 + t) * a.dg_st + ch * a.dg_sj] = s;
-            }
-            cp[ch] = s;
+        for (int idx = tid; idx < C * J; idx += NTB) {
+            const int t = idx / J, ch = idx % J;
+            if (t0 + t < T) dg[(int64_t)(t0 + t) * a.dg_st + ch * a.dg_sj] = sDG[t * DGP + ch];
         }
     }
 }

@@ -62,6 +62,21 @@ __device__ __forceinline__ u32x4 tr_operand(const uint16_t *tile, int krow0, int
     return u32x4{a.x, a.y, b.x, b.y};
 }
 
+// As tr_operand with k in natural order, for operands that pair with rows
+// loaded straight from memory: lane l, k = 8 (l / 32) + e  <->  tile row
+// krow0 + 8 (l / 32) + e (source lane s reads row krow0 + 8 (l / 32) + s / 4,
+// then 4 rows further).  Also conflict-free on TileL<64> and TileL<128>.
+template <int W>
+__device__ __forceinline__ u32x4 tr_operand_lin(const uint16_t *tile, int krow0, int col0, int lane) {
+    const int g = lane >> 4, s = lane & 15;
+    const int i0 = W >= 32 ? 16 * (g & 1) : 0;
+    const int row = krow0 + 8 * (g >> 1) + (s >> 2);
+    const int col = col0 + i0 + 4 * (s & 3);
+    const uint2 a = lds_tr16(tile + TileL<W>::off(row, col));
+    const uint2 b = lds_tr16(tile + TileL<W>::off(row + 4, col));
+    return u32x4{a.x, a.y, b.x, b.y};
+}
+
 // Rows [t0, t0+64) of a [T, W] input matrix, staged global -> registers
 // (fetch, issued a tile ahead) -> LDS (put) as row-major 16-bit operands in the
 // TileL<W> layout, rows past T zero; f32 inputs also keep their bf16 rounding
