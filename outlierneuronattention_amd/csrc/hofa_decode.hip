@@ -34,6 +34,7 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxSplit = 64;  // partials merged per head (one per lane of the merge wave)
 constexpr int kPlanMaxSplit = 48;  // the automatic plan's cap
+constexpr float kRefTau = 16.f;    // a split's softmax reference moves only for scores beyond it by more (log2 units)
 constexpr int kBufFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
 constexpr int kLoadNT = 2;             // non-temporal hint for streamed cache rows
 
@@ -390,17 +391,22 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeKArgs a) 
             const int tok = t0 + (lane + 64 * i) / KL;
             s[i] = tok < we ? acc_s : -INFINITY;
         }
+        // The reference m_run moves (with a wave max and a rescale) only when a
+        // score exceeds it by more than kRefTau; otherwise P <= 2^kRefTau.
         float mt = s[0];
 #pragma unroll
         for (int i = 1; i < NKL; ++i) mt = fmaxf(mt, s[i]);
-        mt = wave_max(mt);
-        const float mn = fmaxf(m_run, mt);
-        const float sc = fast_exp2(m_run - mn);
+        if (__ballot(mt > m_run + kRefTau)) {  // wave-uniform; always taken on the first tile
+            const float mn = fmaxf(m_run, wave_max(mt));
+            const float sc = fast_exp2(m_run - mn);  // 0 while acc and l are still empty
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) acc[e] *= sc;
+            l_run *= sc;
+            m_run = mn;
+        }
         float p[NKL];
 #pragma unroll
-        for (int i = 0; i < NKL; ++i) p[i] = fast_exp2(s[i] - mn);
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) acc[e] *= sc;
+        for (int i = 0; i < NKL; ++i) p[i] = fast_exp2(s[i] - m_run);
         float lsum = 0.f;
 #pragma unroll
         for (int i = 0; i < NVL; ++i) {
@@ -413,8 +419,7 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeKArgs a) 
             for (int e = 0; e < EPV; ++e) acc[e] = fmaf(pi, vf[e], acc[e]);
             lsum += pi;
         }
-        l_run = l_run * sc + lsum;
-        m_run = mn;
+        l_run += lsum;
         if (more) {
 #pragma unroll
             for (int i = 0; i < NKL; ++i) kb[i] = kn[i];
