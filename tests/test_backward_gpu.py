@@ -102,6 +102,7 @@ CASES = [
     (1, 2, 130, 128, 16, False, True, 1.0, torch.float16),
     (1, 2, 160, 64, 16, True, True, 4.0, torch.float32),      # strong decay: element-wise chunk path
     (1, 2, 160, 64, 16, True, True, 4.0, torch.bfloat16),
+    (1, 1, 4200, 64, 16, True, True, 1.0, torch.bfloat16),  # 66 chunks: the per-head suffix runs in two passes
 ]
 
 
@@ -127,11 +128,14 @@ def test_hofa_core_backward_matches_oracle(case):
         _check(out[name], ref[name], tol, f"d{name}")
 
 
-def test_gla_backward_general_decay_matches_oracle():
-    """General per-channel decay g (fla-style), through chunk_gla_inlier_bwd directly."""
+@pytest.mark.parametrize("T", [190, 4200])
+def test_gla_backward_general_decay_matches_oracle(T):
+    """General per-channel decay g (fla-style), through chunk_gla_inlier_bwd directly;
+    T = 4200 spans 66 chunks (more than one pass of the per-head suffix)."""
     from outlierneuronattention_amd.chunk_gla_inlier import (chunk_gla_inlier_bwd, chunk_gla_inlier_fwd,
                                                               chunk_states_numel)
-    B, H, T, D, R = 1, 2, 190, 64, 16
+    print(f"general-decay backward T={T}", flush=True)
+    B, H, D, R = 1, 2, 64, 16
     J = D - R
     gen = torch.Generator().manual_seed(7)
     q, k, v = (torch.randn(B, H, T, D, generator=gen) * 0.5 for _ in range(3))
