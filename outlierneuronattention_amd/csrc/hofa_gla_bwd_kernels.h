@@ -232,8 +232,8 @@ __global__ __launch_bounds__(kScanRows * J / 4) void gla_bwd_scan_kernel(GlaBwdK
 // own rows and the rows of its first loop iteration; a wave whose loop runs
 // twice fetches the second iteration's rows during the first.  For D = 64 the
 // [J][D] hi/lo planes of the exiting (key side) and entering (query side)
-// states go to LDS by DMA in the same phase; the key side reads S_end^T as a
-// transposing read of the same tiles.
+// states go to LDS by DMA after the first barrier; the key side reads S_end^T
+// as a transposing read of the same tiles.
 template <int DT>
 __device__ __forceinline__ void raw_op(const Raw8<DT> &r, u32x4 &hi, u32x4 &lo) {
     if constexpr (DT == HOFA_BF16) {
@@ -315,15 +315,6 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
         for (int ks = 0; ks < DKS; ++ks) iA[ks].load(vrows, t0 + l32, 16 * ks + 8 * hi);  // first sb = 0
     }
-    if constexpr (SLDS) {  // issued last: waiting for the loads above does not wait for these
-        tile::TileDma<64> dm;
-        const uint16_t *src[4] = {dse + 2 * D * J, dse + 3 * D * J, sin + 2 * D * J, sin + 3 * D * J};
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            dm.init(src[p], D, J, w, lane);
-            dm.fetch(sSt[p], 0, w);
-        }
-    }
 
     // ---- decay, then the transposed operand tiles
     const Decay<J, GENERAL> dec{sDec};
@@ -342,6 +333,17 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
         }
     }
     __syncthreads();
+    // The state planes go to LDS by DMA only now: a barrier waits for every
+    // outstanding LDS DMA, so issued earlier they would hold the one above.
+    if constexpr (SLDS) {
+        tile::TileDma<64> dm;
+        const uint16_t *src[4] = {dse + 2 * D * J, dse + 3 * D * J, sin + 2 * D * J, sin + 3 * D * J};
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            dm.init(src[p], D, J, w, lane);
+            dm.fetch(sSt[p], 0, w);
+        }
+    }
 
     auto qval = [&](int ti, int ch) { return t0 + ti < T ? to_f32<DT>(qp[(int64_t)(t0 + ti) * a.f.q_st + R + ch]) : 0.f; };
     auto kval = [&](int ti, int ch) { return t0 + ti < T ? to_f32<DT>(kp[(int64_t)(t0 + ti) * a.f.k_st + R + ch]) : 0.f; };
