@@ -566,21 +566,34 @@ def cpu_model(T: int = 1024, steps: int = 8):
 
 
 def calibrate_copy(nbytes: int = 1 << 30, reps: int = 20):
-    """A plain device-to-device copy of known size: the reference point that
-    scales the FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    """Plain device streams of known size through torch: a copy (read and
+    write 1 GiB: the reference point that scales the FETCH_SIZE / WRITE_SIZE
+    counters to bytes), a sum (read only) and an add (two reads per write).
+    Their rates are the practical HBM ceilings for a kernel's read/write mix."""
     src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for _ in range(reps):
-        dst.copy_(src)
-    t1.record()
-    torch.cuda.synchronize()
-    s = t0.elapsed_time(t1) / 1e3 / reps
-    return dict(bytes_read=nbytes, bytes_written=nbytes, us=round(s * 1e6, 2), gbs=round(2 * nbytes / s / 1e9, 1))
+    half = nbytes // 8  # add: two inputs and one output of half the size each
+
+    def rate(fn, moved):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        s = t0.elapsed_time(t1) / 1e3 / reps
+        return s, round(moved / s / 1e9, 1)
+
+    s, copy_gbs = rate(lambda: dst.copy_(src), 2 * nbytes)
+    acc = torch.empty((), dtype=torch.float32, device="cuda")
+    _, read_gbs = rate(lambda: torch.sum(src, dim=0, out=acc), nbytes)
+    a, b, c = src[:half], src[half:2 * half], dst[:half]
+    _, add_gbs = rate(lambda: torch.add(a, b, out=c), 3 * half * 4)
+    return dict(bytes_read=nbytes, bytes_written=nbytes, us=round(s * 1e6, 2), gbs=copy_gbs,
+                read_only_gbs=read_gbs, two_reads_per_write_gbs=add_gbs)
 
 
 def _traffic_from_profile(name: str):
