@@ -1,6 +1,7 @@
 // Pieces shared by the chunked GLA forward (hofa_gla.hip) and backward
-// (hofa_gla_bwd.hip): chunk constants, the in-chunk decay cumsum, transposed
-// LDS staging, and the per-chunk outer-product kernel used by both passes
+// (hofa_gla_bwd.hip): chunk constants, the in-chunk decay cumsum, two-phase
+// (issue, then commit) transposed LDS staging, and the per-chunk
+// outer-product kernel used by both passes
 // (forward: dS^T = V^T (K (.) exp(G_last - G)); backward: dH^T = dO^T (Q (.) exp(G))).
 #pragma once
 
@@ -18,29 +19,6 @@ constexpr float kSafeRange = 64.f;  // max in-chunk -G for factored exp(+-G) ope
 constexpr int OPB = HOFA_BF16;
 template <int DT> constexpr bool kRawSplit = DT != HOFA_BF16;
 
-// 8 consecutive input elements -> bf16 operand hi and the rounding remainder lo
-// (lo is zero for bf16 inputs).
-template <int DT>
-__device__ __forceinline__ void raw_op8(const typename Stor<DT>::type *p, u32x4 &hi, u32x4 &lo) {
-    if constexpr (DT == HOFA_BF16) {
-        hi = *(const u32x4 *)p;
-        lo = u32x4{0, 0, 0, 0};
-    } else {
-        float x[8];
-        if constexpr (DT == HOFA_F32) {
-            const f32x4 u = *(const f32x4 *)p, w = *(const f32x4 *)(p + 4);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[e] = u[e];
-                x[4 + e] = w[e];
-            }
-        } else {
-            unpack16<DT>(*(const u32x4 *)p, x);
-        }
-        split8<OPB>(x, hi, lo);
-    }
-}
-
 // The T rows of one head's [T, *] operand through a range-checked buffer:
 // rows at or past T read as zeros, so tile loads need no branches.  The
 // base pointer must be wave-uniform; the host checks that (T + 2C) rows span
@@ -53,31 +31,6 @@ struct Rows {
     __device__ Rows(const in_t *base, int64_t row_stride, int T)
         : r(rows_rsrc(base, (uint32_t)(T * row_stride * (int64_t)sizeof(in_t)))), st(row_stride) {}
     __device__ uint32_t off(int row, int col) const { return (uint32_t)((row * st + col) * (int64_t)sizeof(in_t)); }
-    // 8 elements [col, col+8) of a row as floats
-    __device__ void f8(int row, int col, float *x) const {
-        const u32x4 a = bload16(r, off(row, col));
-        if constexpr (DT == HOFA_F32) {
-            const u32x4 b = bload16(r, off(row, col) + 16);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[e] = __uint_as_float(a[e]);
-                x[4 + e] = __uint_as_float(b[e]);
-            }
-        } else {
-            unpack16<DT>(a, x);
-        }
-    }
-    // 8 elements as a bf16 operand quad hi and the rounding remainder lo (zero for bf16)
-    __device__ void op8(int row, int col, u32x4 &hi, u32x4 &lo) const {
-        if constexpr (DT == HOFA_BF16) {
-            hi = bload16(r, off(row, col));
-            lo = u32x4{0, 0, 0, 0};
-        } else {
-            float x[8];
-            f8(row, col, x);
-            split8<HOFA_BF16>(x, hi, lo);
-        }
-    }
 };
 
 // Four consecutive outputs (16-byte aligned for f32, 8-byte for 16-bit types).
@@ -134,107 +87,13 @@ struct Decay {
         else return s[t] * s[C + c];
     }
     __device__ __forceinline__ float last(int c) const { return G(C - 1, c); }
-    // Largest |G| over the chunk (valid after load_decay).
+    // Largest |G| over the chunk (valid after DecayStage::commit).
     __device__ __forceinline__ float range() const {
         const float *r = s + kBody;
         if constexpr (GENERAL) return fmaxf(fmaxf(r[0], r[1]), fmaxf(r[2], r[3]));
         else return r[0] * r[1];
     }
 };
-
-// Fill a Decay for chunk [t0, t0+C) of head (b, h); ends with a barrier.  NTH
-// threads, 128 <= NTH <= 256.
-template <int J, bool GENERAL, int NTH>
-__device__ void load_decay(const GlaK &a, int b, int h, int t0, Decay<J, GENERAL> dec) {
-    static_assert(NTH >= 128 && NTH <= 256, "two to four waves");
-    constexpr int NW = NTH / 64;
-    float *s = dec.s, *red = s + Decay<J, GENERAL>::kBody;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    if constexpr (!GENERAL) {
-        if (w == 0) {
-            const int t = t0 + lane;
-            float x = t < a.T ? load_any(a.lg, a.lg_dt, b * a.lg_sb + h * a.lg_sh + (int64_t)t * a.lg_st) : 0.f;
-            x = wave_incl_scan(x);
-            s[lane] = x;
-            const float m = wave_max(fabsf(x));
-            if (lane == 0) red[0] = m;
-        } else if (w == 1) {
-            float m = 0.f;
-            for (int c = lane; c < J; c += 64) {
-                const float al = a.la ? expf(load_any(a.la, a.la_dt, h * a.la_sh + c * a.la_sj)) : 1.f;
-                s[C + c] = al;
-                m = fmaxf(m, al);
-            }
-            m = wave_max(m);
-            if (lane == 0) red[1] = m;
-        }
-        __syncthreads();
-    } else {
-        const float *gp = (const float *)a.g + b * a.g_sb + h * a.g_sh;
-        const bool vec = a.g_sj == 1 && (a.g_st % 4) == 0 && (a.g_sb % 4) == 0 && (a.g_sh % 4) == 0 &&
-                         ((uintptr_t)a.g % 16) == 0;
-        for (int idx = tid; idx < C * J / 4; idx += NTH) {
-            const int t = idx / (J / 4), c = 4 * (idx % (J / 4));
-            f32x4 x = {0.f, 0.f, 0.f, 0.f};
-            if (t0 + t < a.T) {
-                const float *p = gp + (int64_t)(t0 + t) * a.g_st;
-                if (vec) {
-                    x = *(const f32x4 *)(p + c);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) x[e] = p[(c + e) * a.g_sj];
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) s[t * Decay<J, GENERAL>::GP + c + e] = x[e];
-        }
-        if (tid < 4) red[tid] = 0.f;
-        __syncthreads();
-        float m = 0.f;
-        constexpr int NCOL = (J + NW - 1) / NW;
-#pragma unroll
-        for (int i = 0; i < NCOL; ++i) {  // columns w, w + NW, ..: lane = token; independent chains
-            const int c = w + i * NW;
-            if (J % NW == 0 || c < J) {
-                const float x = wave_incl_scan(s[lane * Decay<J, GENERAL>::GP + c]);
-                s[lane * Decay<J, GENERAL>::GP + c] = x;
-                m = fmaxf(m, fabsf(x));
-            }
-        }
-        m = wave_max(m);
-        if (lane == 0) red[w] = m;
-        __syncthreads();
-    }
-}
-
-// Copy one chunk of rows [t0, t0+C) x columns [col0, col0+W) into LDS
-// transposed ([W][pitch] bf16 operands), scaled per element; with LO the
-// rounding remainder goes to dst_lo.  Rows past T are zero.
-template <int DT, int W, int PITCH, bool LO, int NTH, typename Scale>
-__device__ void load_transposed(const typename Stor<DT>::type *base, int64_t row_stride, int col0, int t0, int T,
-                                uint16_t *dst, uint16_t *dst_lo, Scale scale) {
-    constexpr int NPIECE = (C / 2) * (W / 8);
-    const Rows<DT> rows(base, row_stride, T);
-    for (int pi = threadIdx.x; pi < NPIECE; pi += NTH) {
-        const int tp = pi / (W / 8), cc = pi % (W / 8);
-        const int t = 2 * tp;
-        float x[2][8];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            rows.f8(t0 + t + r, col0 + 8 * cc, x[r]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) x[r][e] *= scale(t + r, 8 * cc + e);
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t hv = pack2<OPB>(x[0][e], x[1][e]);
-            *(uint32_t *)&dst[(8 * cc + e) * PITCH + t] = hv;
-            if constexpr (LO)
-                *(uint32_t *)&dst_lo[(8 * cc + e) * PITCH + t] =
-                    pack2<OPB>(x[0][e] - op_to_f32<OPB>(hv & 0xffffu), x[1][e] - op_to_f32<OPB>(hv >> 16));
-        }
-    }
-}
 
 // ---- two-phase staging: issue() starts a tile's global loads into registers,
 // commit() writes it to LDS later, so that the loads of every tile of a chunk
@@ -264,7 +123,7 @@ struct Raw8 {
 
 // A [C x W] chunk tile (columns [col0, col0+W)) in pieces of 2 rows x 8
 // columns per thread, committed to LDS transposed ([W][PITCH] 16-bit
-// operands, tokens contiguous) like load_transposed.
+// operands, tokens contiguous); rows past T are zero.
 template <int DT, int W, int NTH>
 struct TrStage {
     static constexpr int NPIECE = (C / 2) * (W / 8);
@@ -311,8 +170,9 @@ struct TrStage {
     }
 };
 
-// The decay of one chunk: issue() loads it into registers, commit() fills a
-// Decay exactly as load_decay does (ends with a barrier).
+// The decay of chunk [t0, t0+C) of head (b, h): issue() loads it into
+// registers, commit() fills a Decay (ends with a barrier).  NTH threads,
+// 128 <= NTH <= 256.
 template <int J, bool GENERAL, int NTH>
 struct DecayStage {
     static_assert(NTH >= 128 && NTH <= 256, "two to four waves");
