@@ -27,7 +27,7 @@
 //                               2 query-side waves (dq); dGamma reductions
 //                               (a factored launch and an element-wise launch for
 //                               chunks with a decay range beyond kSafeRange)
-//   5. gla_bwd_dlg_kernel       per (batch, head): later-chunk suffix of d log_gamma / d g,
+//   5. gla_bwd_dlg_kernel       per (batch, head) and 256-token slice: later-chunk suffix of d log_gamma / d g,
 //                               d log_alpha and d gla_scale partials
 //   6. gla_bwd_param_kernel     per head: d gla_scale, d log_alpha (sum over the batch)
 // Every matrix-core product takes bf16 operands; computed operands are hi/lo
@@ -49,6 +49,10 @@ using namespace gla;
 constexpr int NTB = 256;   // threads of the chunk backward kernel
 constexpr int ET = 256;    // tokens per epilogue block
 constexpr int kMaxChunks = 4096;
+// The chunk kernel stages the [J][D] state planes in LDS (one 64-row tile
+// each) and reads them transposed where it needs S^T, so planes 0/1 of the
+// backward states are never read.
+template <int D, int J> constexpr bool kStateLds = D == 64 && J <= 64;
 
 struct GlaBwdK {
     GlaK f;  // forward inputs: q, k, v, lg, la, g, mix, gs with strides; B, H, T, R, nc
@@ -214,8 +218,9 @@ __global__ __launch_bounds__(kScanRows * J / 4) void gla_bwd_scan_kernel(GlaBwdK
         for (int u = 0; u < PF; ++u) {
             const int c = c0 - u;
             if (c < 0) break;  // block-uniform
-            store_state_tile<DT, D, J>(a.ds_end + (base + c) * 4 * D * J, 4, dv0, dvl, j4, X, sT[c & 1][0],
-                                       sT[c & 1][1]);
+            // the chunk kernel reads dH_end^T (planes 0/1) only without kStateLds
+            store_state_tile<DT, D, J, !kStateLds<D, J>>(a.ds_end + (base + c) * 4 * D * J, 4, dv0, dvl, j4, X,
+                                                        sT[c & 1][0], sT[c & 1][1]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) X[e] = fmaf(fast_exp2(gl[u][e] * kLog2e), X[e], dh[u][e]);
         }
@@ -259,7 +264,7 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
     constexpr bool SPL = kRawSplit<DT>;   // raw f32/f16 inputs are split as well
     constexpr int NO = SPL ? 2 : 1;
     constexpr int DGP = J + 1;             // pitch of the dGamma tile
-    constexpr bool SLDS = D == 64 && J <= 64;  // state planes staged in LDS (one 64-row tile each)
+    constexpr bool SLDS = kStateLds<D, J>;  // state planes staged in LDS (one 64-row tile each)
     static_assert(NTB == tile::NT, "the state DMA splits each tile over four waves");
     __shared__ float sDec[Decay<J, GENERAL>::kFloats];
     __shared__ __attribute__((aligned(16))) uint16_t sQK[2][2][JP * TP];  // [Q~^T | K~^T][hi | lo]
@@ -791,91 +796,100 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
 }
 
 // ---------------------------------------------------------------- 5. per-head suffix and partials
-// One block per (b, h): adds the later-chunk suffix to d log_gamma (or d g),
-// and reduces this head's d log_alpha / d gla_scale partials over chunks and
-// token tiles.
+// Grid (B*H, kDlgTokens-token slices + 2).  A slice block adds the
+// later-chunk suffix to d log_gamma (or d g) of its tokens; block NSL
+// reduces this head's d log_alpha partials over chunks, block NSL + 1 its
+// d gla_scale partials over token tiles.  Every block has one short chain of
+// loads (96 heads of one block each left the GPU waiting on four in a row).
+constexpr int kDlgTokens = 256;  // tokens per slice block
+constexpr int kDlgChunks = kDlgTokens / C;
+
 template <int D, int J, bool GENERAL>
 __global__ __launch_bounds__(256) void gla_bwd_dlg_kernel(GlaBwdK a) {
-    __shared__ float sSfx[kMaxChunks];   // sum of e over later chunks
-    __shared__ float sLst[kMaxChunks];   // cumsum of log_gamma before the chunk
+    __shared__ float sLst[kMaxChunks];            // cumsum of log_gamma before the chunk (d log_alpha block)
+    __shared__ float sSfx[kDlgChunks][GENERAL ? J : 1];  // suffix over later chunks, per chunk of the slice
     __shared__ float sRed[256];
     constexpr int CPS = 2 * J + 2;
     const int bh = blockIdx.x, H = a.f.H, T = a.f.T, nc = a.f.nc;
     const int b = bh / H, h = bh % H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    float *cp = a.chunk_part + (int64_t)bh * nc * CPS;
-    if constexpr (!GENERAL) {
-        if (w == 0) {  // exclusive suffix of the per-chunk e totals
-            float carry = 0.f;
-            for (int top = nc - 1; top >= 0; top -= 64) {
-                const int c = top - lane;
-                const float e = c >= 0 ? cp[(int64_t)c * CPS + 2 * J] : 0.f;
-                float x = e;
-#pragma unroll
-                for (int off = 1; off < 64; off <<= 1) {
-                    const float y = __shfl_up(x, off);
-                    if (lane >= off) x += y;
+    const int nsl = (T + kDlgTokens - 1) / kDlgTokens;
+    const int y = blockIdx.y;
+    const float *cp = a.chunk_part + (int64_t)bh * nc * CPS;
+    if (y < nsl) {
+        const int c_lo = y * kDlgChunks, c_hi = min(nc, c_lo + kDlgChunks);
+        if constexpr (!GENERAL) {
+            // sum of e over the chunks past the slice, then the slice's own suffixes
+            float part = 0.f;
+            for (int c = c_hi + tid; c < nc; c += 256) part += cp[(int64_t)c * CPS + 2 * J];
+            part = wave_sum(part);
+            if (lane == 0) sRed[w] = part;
+            __syncthreads();
+            if (tid == 0) {
+                float carry = sRed[0] + sRed[1] + sRed[2] + sRed[3];
+                for (int c = c_hi - 1; c >= c_lo; --c) {
+                    sSfx[c - c_lo][0] = carry;
+                    carry += cp[(int64_t)c * CPS + 2 * J];
                 }
-                if (c >= 0) sSfx[c] = carry + x - e;
-                carry += __shfl(x, 63);
             }
-        } else if (w == 1) {  // exclusive prefix of the per-chunk log_gamma totals
+            __syncthreads();
+            const int t = y * kDlgTokens + tid;
+            if (t < T)
+                store_any(a.dlg, a.dlg_dt, b * a.dlg_sb + h * a.dlg_sh + (int64_t)t * a.dlg_st,
+                          a.dlg_part[(int64_t)bh * T + t] + sSfx[t / C - c_lo][0]);
+        } else {
+            // per channel: sum over the chunks past the slice, then the slice's own suffixes
+            for (int ch = tid; ch < J; ch += 256) {
+                float carry = 0.f;
+                for (int c = c_hi; c < nc; ++c) carry += cp[(int64_t)c * CPS + ch];
+                for (int c = c_hi - 1; c >= c_lo; --c) {
+                    sSfx[c - c_lo][ch] = carry;
+                    carry += cp[(int64_t)c * CPS + ch];
+                }
+            }
+            __syncthreads();
+            float *dg = (float *)a.dg + b * a.dg_sb + h * a.dg_sh;
+            const int t0 = y * kDlgTokens, nt = min(kDlgTokens, T - t0);
+            for (int i = tid; i < nt * J; i += 256) {
+                const int t = t0 + i / J, ch = i % J;
+                dg[(int64_t)t * a.dg_st + ch * a.dg_sj] += sSfx[t / C - c_lo][ch];
+            }
+        }
+    } else if (y == nsl) {
+        // sum_c (Lambda_start(c) sum_t dGamma + sum_t dGamma Lambda_in), channel-parallel
+        if (GENERAL || !a.dla) return;
+        if (w == 0) {  // exclusive prefix of the per-chunk log_gamma totals
             float carry = 0.f;
             for (int c0 = 0; c0 < nc; c0 += 64) {
                 const int c = c0 + lane;
                 const float l = c < nc ? cp[(int64_t)c * CPS + 2 * J + 1] : 0.f;
-                float x = l;
-#pragma unroll
-                for (int off = 1; off < 64; off <<= 1) {
-                    const float y = __shfl_up(x, off);
-                    if (lane >= off) x += y;
-                }
+                const float x = wave_incl_scan(l);
                 if (c < nc) sLst[c] = carry + x - l;
                 carry += __shfl(x, 63);
             }
         }
         __syncthreads();
-        for (int t = tid; t < T; t += 256)
-            store_any(a.dlg, a.dlg_dt, b * a.dlg_sb + h * a.dlg_sh + (int64_t)t * a.dlg_st,
-                      a.dlg_part[(int64_t)bh * T + t] + sSfx[t / C]);
-        if (a.dla) {  // sum_c (Lambda_start(c) sum_t dGamma + sum_t dGamma Lambda_in), channel-parallel
-            constexpr int NSEG = 256 / J;
-            const int ch = tid % J, seg = tid / J;
-            float acc = 0.f;
-            if (seg < NSEG)
-                for (int c = seg; c < nc; c += NSEG) {
-                    const float *p = cp + (int64_t)c * CPS;
-                    acc = fmaf(sLst[c], p[ch], acc + p[J + ch]);
-                }
-            sRed[tid] = acc;
-            __syncthreads();
-            if (tid < J) {
-                float t = 0.f;
-                for (int sg = 0; sg < NSEG; ++sg) t += sRed[sg * J + tid];
-                a.part_la[(int64_t)bh * J + tid] = t;
+        constexpr int NSEG = 256 / J;
+        const int ch = tid % J, seg = tid / J;
+        float acc = 0.f;
+        if (seg < NSEG)
+            for (int c = seg; c < nc; c += NSEG) {
+                const float *p = cp + (int64_t)c * CPS;
+                acc = fmaf(sLst[c], p[ch], acc + p[J + ch]);
             }
+        sRed[tid] = acc;
+        __syncthreads();
+        if (tid < J) {
+            float t = 0.f;
+            for (int sg = 0; sg < NSEG; ++sg) t += sRed[sg * J + tid];
+            a.part_la[(int64_t)bh * J + tid] = t;
         }
     } else {
-        for (int ch = tid; ch < J; ch += 256) {
-            float carry = 0.f;
-            for (int c = nc - 1; c >= 0; --c) {
-                float *p = cp + (int64_t)c * CPS + ch;
-                const float x = *p;
-                *p = carry;
-                carry += x;
-            }
+        for (int d = tid; d < D; d += 256) {
+            float s = 0.f;
+            for (int tile = 0; tile < a.ntile; ++tile) s += a.dgs_part[((int64_t)bh * a.ntile + tile) * D + d];
+            a.part_gs[(int64_t)bh * D + d] = s;
         }
-        __syncthreads();
-        float *dg = (float *)a.dg + b * a.dg_sb + h * a.dg_sh;
-        for (int64_t i = tid; i < (int64_t)T * J; i += 256) {
-            const int t = (int)(i / J), ch = (int)(i % J);
-            dg[(int64_t)t * a.dg_st + ch * a.dg_sj] += cp[(int64_t)(t / C) * CPS + ch];
-        }
-    }
-    for (int d = tid; d < D; d += 256) {
-        float s = 0.f;
-        for (int tile = 0; tile < a.ntile; ++tile) s += a.dgs_part[((int64_t)bh * a.ntile + tile) * D + d];
-        a.part_gs[(int64_t)bh * D + d] = s;
     }
 }
 
@@ -915,7 +929,8 @@ void launch(const GlaBwdK &k, hipStream_t s) {
     hipLaunchKernelGGL((gla_bwd_scan_kernel<DT, D, J>), dim3(nbh, D / kScanRows), dim3(kScanRows * J / 4), 0, s, k);
     hipLaunchKernelGGL((gla_bwd_chunk_kernel<DT, D, J, GEN, false>), dim3(nbh * k.f.nc), dim3(NTB), 0, s, k);
     hipLaunchKernelGGL((gla_bwd_chunk_kernel<DT, D, J, GEN, true>), dim3(nbh * k.f.nc), dim3(NTB), 0, s, k);
-    hipLaunchKernelGGL((gla_bwd_dlg_kernel<D, J, GEN>), dim3(nbh), dim3(256), 0, s, k);
+    hipLaunchKernelGGL((gla_bwd_dlg_kernel<D, J, GEN>), dim3(nbh, (k.f.T + kDlgTokens - 1) / kDlgTokens + 2),
+                       dim3(256), 0, s, k);
     hipLaunchKernelGGL((gla_bwd_param_kernel<D, J, GEN>), dim3(k.f.H), dim3(256), 0, s, k);
 }
 

@@ -373,11 +373,13 @@ constexpr int kScanPitch = kScanRows + 4;  // LDS row pitch: 8-byte aligned rows
 // directly; with four planes, planes 2/3 (S, d contiguous) through the LDS tile
 // sT[2][J * kScanPitch] (hi, lo), so that they also leave with contiguous
 // stores.  Contains a barrier when nplanes == 4 (block-uniform); callers
-// alternate between two tiles, so one barrier per chunk suffices.
-template <int DT, int D, int J>
+// alternate between two tiles, so one barrier per chunk suffices.  Without
+// TPLANES (four planes only) planes 0/1 are left unwritten, for a consumer
+// that reads only planes 2/3.
+template <int DT, int D, int J, bool TPLANES = true>
 __device__ __forceinline__ void store_state_tile(uint16_t *dst, int nplanes, int dv0, int dvl, int j4,
                                                  const f32x4 &S, uint16_t *th, uint16_t *tl) {
-    store_state_planes(dst, nplanes, D, J, dv0 + dvl, j4, S);
+    if (TPLANES || nplanes != 4) store_state_planes(dst, nplanes, D, J, dv0 + dvl, j4, S);
     if (nplanes != 4) return;
     uint2 hv, lv;
     split4(S, hv, lv);
