@@ -186,7 +186,8 @@ int hofa_attn_fwd(const hofa_attn_fwd_args_t *args, void *stream);
  *   chunk_states   optional 16-bit [B*H][ceil(T/64)][4][D*J] receiving the
  *                  state that enters each chunk as bf16 hi/lo operand pairs
  *                  (hi + lo ~ the fp32 state): planes 0/1 transposed [D][J],
- *                  planes 2/3 as [J][D]; saved for hofa_gla_bwd
+ *                  planes 2/3 as [J][D] (written for D = 128 only: for D = 64 the
+ *                  backward reads S from the S^T planes); saved for hofa_gla_bwd
  *   n_out          optional [B,H,T,D] (dtype of y): RMSNorm(Y_I) before the
  *                  gate, saved for hofa_gla_bwd (needs fuse_norm_gate)
  *   rstd           float32 [B*H*T] receiving 1/sqrt(mean(Y_I^2) + eps) when

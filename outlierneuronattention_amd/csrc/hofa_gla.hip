@@ -68,8 +68,8 @@ __global__ __launch_bounds__(kScanRows * J / 4) void gla_scan_kernel(GlaK a) {
             if (c >= nc) break;  // block-uniform
             const f32x4 d = ds[u], g = gl[u];
             fetch(u, c + kScanPF);
-            store_state_tile<DT, D, J>(a.s_in + (base + c) * a.nplanes * D * J, a.nplanes, dv0, dvl, j4, S,
-                                       sT[c & 1][0], sT[c & 1][1]);
+            store_state_tile<DT, D, J>(a.s_in + (base + c) * a.nplanes * D * J, planes_written<D, J>(a.nplanes), dv0,
+                                       dvl, j4, S, sT[c & 1][0], sT[c & 1][1]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) S[e] = fmaf(fast_exp2(g[e] * kLog2e), S[e], d[e]);
         }

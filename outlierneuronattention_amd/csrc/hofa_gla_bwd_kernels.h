@@ -49,10 +49,7 @@ using namespace gla;
 constexpr int NTB = 256;   // threads of the chunk backward kernel
 constexpr int ET = 256;    // tokens per epilogue block
 constexpr int kMaxChunks = 4096;
-// The chunk kernel stages the [J][D] state planes in LDS (one 64-row tile
-// each) and reads them transposed where it needs S^T, so planes 0/1 of the
-// backward states are never read.
-template <int D, int J> constexpr bool kStateLds = D == 64 && J <= 64;
+
 
 struct GlaBwdK {
     GlaK f;  // forward inputs: q, k, v, lg, la, g, mix, gs with strides; B, H, T, R, nc
@@ -218,9 +215,8 @@ __global__ __launch_bounds__(kScanRows * J / 4) void gla_bwd_scan_kernel(GlaBwdK
         for (int u = 0; u < PF; ++u) {
             const int c = c0 - u;
             if (c < 0) break;  // block-uniform
-            // the chunk kernel reads dH_end^T (planes 0/1) only without kStateLds
-            store_state_tile<DT, D, J, !kStateLds<D, J>>(a.ds_end + (base + c) * 4 * D * J, 4, dv0, dvl, j4, X,
-                                                        sT[c & 1][0], sT[c & 1][1]);
+            store_state_tile<DT, D, J>(a.ds_end + (base + c) * 4 * D * J, planes_written<D, J>(4), dv0, dvl, j4, X,
+                                       sT[c & 1][0], sT[c & 1][1]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) X[e] = fmaf(fast_exp2(gl[u][e] * kLog2e), X[e], dh[u][e]);
         }
@@ -236,9 +232,9 @@ __global__ __launch_bounds__(kScanRows * J / 4) void gla_bwd_scan_kernel(GlaBwdK
 // decay, the three transposed operand tiles (Q~^T, K~^T, dO^T), each side's
 // own rows and the rows of its first loop iteration; a wave whose loop runs
 // twice fetches the second iteration's rows during the first.  For D = 64 the
-// [J][D] hi/lo planes of the exiting (key side) and entering (query side)
-// states go to LDS by DMA after the first barrier; the key side reads S_end^T
-// as a transposing read of the same tiles.
+// S^T ([D][J]) hi/lo planes of the exiting (key side) and entering (query
+// side) states go to LDS by DMA after the first barrier; S itself is a
+// transposing read of the same tiles, so planes 2/3 are neither written nor read.
 template <int DT>
 __device__ __forceinline__ void raw_op(const Raw8<DT> &r, u32x4 &hi, u32x4 &lo) {
     if constexpr (DT == HOFA_BF16) {
@@ -269,7 +265,7 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
     __shared__ float sDec[Decay<J, GENERAL>::kFloats];
     __shared__ __attribute__((aligned(16))) uint16_t sQK[2][2][JP * TP];  // [Q~^T | K~^T][hi | lo]
     __shared__ __attribute__((aligned(16))) uint16_t sOt[NO][D * TP];     // dO^T
-    // [S_end hi, S_end lo, S_in hi, S_in lo], each [J][D] in the TileL<64> layout
+    // [S_end hi, S_end lo, S_in hi, S_in lo], each S^T [D][J] in the TileL<64> layout
     __shared__ __attribute__((aligned(16))) uint16_t sSt[SLDS ? 4 : 1][SLDS ? TileL<64>::ELEMS : 8];
     static_assert(sizeof(sQK) >= sizeof(float) * C * DGP, "dGamma reuses the operand tiles");
     static_assert(sizeof(sOt) >= sizeof(float) * 2 * NTB, "the channel sums reuse the dO tile");
@@ -340,12 +336,12 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
     __syncthreads();
     // The state planes go to LDS by DMA only now: a barrier waits for every
     // outstanding LDS DMA, so issued earlier they would hold the one above.
-    if constexpr (SLDS) {
-        tile::TileDma<64> dm;
-        const uint16_t *src[4] = {dse + 2 * D * J, dse + 3 * D * J, sin + 2 * D * J, sin + 3 * D * J};
+    if constexpr (SLDS) {  // S^T planes ([D][J], J columns of a 64-wide tile; the rest zero)
+        tile::TileDma<64, J> dm;
+        const uint16_t *src[4] = {dse, dse + D * J, sin, sin + D * J};
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            dm.init(src[p], D, J, w, lane);
+            dm.init(src[p], J, D, w, lane);
             dm.fetch(sSt[p], 0, w);
         }
     }
@@ -357,13 +353,15 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
     auto staged = [&](int which, int ch, int tk) {
         return op_to_f32<OPB>(sQK[which][0][ch * TP + tk]) + op_to_f32<OPB>(sQK[which][1][ch * TP + tk]);
     };
-    // S rows (channel cr, 8 value columns from col) of a [J][D] state plane pair
-    auto state_row = [&](int which, const uint16_t *g2, int cr, int col, u32x4 &sh, u32x4 &sl) {
+    // A operand S[c][d] (rows c = 32 jb + lane%32, k = d = 16 ks + 8 hi + e) of a
+    // state plane pair: a transposing read of the staged S^T tiles, or rows of
+    // the [J][D] planes 2/3 in memory
+    auto state_row = [&](int which, const uint16_t *g2, int jb, int ks, u32x4 &sh, u32x4 &sl) {
         if constexpr (SLDS) {
-            const int o = TileL<64>::off(cr, col);
-            sh = *(const u32x4 *)&sSt[2 * which][o];
-            sl = *(const u32x4 *)&sSt[2 * which + 1][o];
+            sh = tile::tr_operand_lin<64>(sSt[2 * which], 16 * ks, 32 * jb, lane);
+            sl = tile::tr_operand_lin<64>(sSt[2 * which + 1], 16 * ks, 32 * jb, lane);
         } else {
+            const int cr = 32 * jb + l32, col = 16 * ks + 8 * hi;
             sh = cr < J ? *(const u32x4 *)(g2 + cr * D + col) : zero4;
             sl = cr < J ? *(const u32x4 *)(g2 + D * J + cr * D + col) : zero4;
         }
@@ -520,13 +518,12 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
         // X = sum_d dH_end[c, d] V[s, d]; acc then holds this key's part of dGamma, -k dk
 #pragma unroll
         for (int jb = 0; jb < JB; ++jb) {
-            const int cr = 32 * jb + l32;
             f32x16 x = {};
             if (c < nc - 1) {
 #pragma unroll
                 for (int ks = 0; ks < DKS; ++ks) {
                     u32x4 sh, sl;
-                    state_row(0, dse + 2 * D * J, cr, 16 * ks + 8 * hi, sh, sl);
+                    state_row(0, dse + 2 * D * J, jb, ks, sh, sl);
                     x = mfma32<OPB>(sh, vh[ks], x);
                     x = mfma32<OPB>(sl, vh[ks], x);
                     if constexpr (SPL) x = mfma32<OPB>(sh, vl[ks], x);
@@ -571,9 +568,10 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb) {
                     u32x4 sh, sl;
-                    if constexpr (SLDS) {  // A[d, c] = S_end[c][d]: transposing reads of the state tiles
-                        sh = tile::tr_operand_lin<64>(sSt[0], 16 * ks, 32 * mb, lane);
-                        sl = tile::tr_operand_lin<64>(sSt[1], 16 * ks, 32 * mb, lane);
+                    if constexpr (SLDS) {  // A[d, c] = S_end^T rows of the staged tiles
+                        const int o = TileL<64>::off(32 * mb + l32, 16 * ks + 8 * hi);
+                        sh = *(const u32x4 *)&sSt[0][o];
+                        sl = *(const u32x4 *)&sSt[1][o];
                     } else {
                         const int off = (32 * mb + l32) * J + 16 * ks + 8 * hi;
                         sh = *(const u32x4 *)(dse + off);
@@ -669,7 +667,6 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
         // dq^T[c, t] (+)= e^G_tc (sum_d S_in[c, d] dO[t, d])
 #pragma unroll
         for (int jb = 0; jb < JB; ++jb) {
-            const int cr = 32 * jb + l32;
             f32x16 x;
 #pragma unroll
             for (int v = 0; v < 16; ++v) x[v] = 0.f;
@@ -677,7 +674,7 @@ __global__ __launch_bounds__(NTB, 2) void gla_bwd_chunk_kernel(GlaBwdK a) {
 #pragma unroll
                 for (int ks = 0; ks < DKS; ++ks) {
                     u32x4 sh, sl;
-                    state_row(1, sin + 2 * D * J, cr, 16 * ks + 8 * hi, sh, sl);
+                    state_row(1, sin + 2 * D * J, jb, ks, sh, sl);
                     x = mfma32<OPB>(sh, dh[ks], x);
                     x = mfma32<OPB>(sl, dh[ks], x);
                     if constexpr (SPL) x = mfma32<OPB>(sh, dl[ks], x);

@@ -281,6 +281,13 @@ struct DecayStage {
     }
 };
 
+// A backward pass (chunk_states, four planes per chunk) with D = 64 stages
+// the S^T planes in LDS and reads S there with transposing loads, so only
+// planes 0/1 are written; D = 128 reads all four planes from memory.
+template <int D, int J> constexpr bool kStateLds = D == 64 && J <= 64;
+template <int D, int J>
+__host__ __device__ constexpr int planes_written(int nplanes) { return nplanes == 4 && kStateLds<D, J> ? 2 : nplanes; }
+
 constexpr int kStateThreads = 256;  // four waves: the LDS footprint allows four blocks per CU
 
 // Per chunk: in-chunk cumsum G of the log decay, then
@@ -373,13 +380,11 @@ constexpr int kScanPitch = kScanRows + 4;  // LDS row pitch: 8-byte aligned rows
 // directly; with four planes, planes 2/3 (S, d contiguous) through the LDS tile
 // sT[2][J * kScanPitch] (hi, lo), so that they also leave with contiguous
 // stores.  Contains a barrier when nplanes == 4 (block-uniform); callers
-// alternate between two tiles, so one barrier per chunk suffices.  Without
-// TPLANES (four planes only) planes 0/1 are left unwritten, for a consumer
-// that reads only planes 2/3.
-template <int DT, int D, int J, bool TPLANES = true>
+// alternate between two tiles, so one barrier per chunk suffices.
+template <int DT, int D, int J>
 __device__ __forceinline__ void store_state_tile(uint16_t *dst, int nplanes, int dv0, int dvl, int j4,
                                                  const f32x4 &S, uint16_t *th, uint16_t *tl) {
-    if (TPLANES || nplanes != 4) store_state_planes(dst, nplanes, D, J, dv0 + dvl, j4, S);
+    store_state_planes(dst, nplanes, D, J, dv0 + dvl, j4, S);
     if (nplanes != 4) return;
     uint2 hv, lv;
     split4(S, hv, lv);

@@ -119,8 +119,9 @@ struct TileStage {
 // the source granule that the TileL<W> swizzle puts at its position; padding
 // granules (W = 16) and rows past T read out of range and land as zeros.
 // The loads count against vmcnt: the issuing wave waits for them before the
-// barrier that hands the buffer to the block.
-template <int W>
+// barrier that hands the buffer to the block.  SRCW < W: source rows of SRCW
+// elements (a multiple of 8) fill the first SRCW columns, the rest read zeros.
+template <int W, int SRCW = W>
 struct TileDma {
     static constexpr int GPR = TileL<W>::PITCH / 8;  // 16-byte granules per LDS row, padding included
     static constexpr int NLOAD = GPR;                 // 64 rows x GPR granules / 64 lanes
@@ -138,8 +139,8 @@ struct TileDma {
         for (int j = 0; j < NW; ++j) {
             const int p = 64 * (4 * j + wave) + lane;
             const int row = p / GPR, pg = p % GPR;
-            voff[j] = pg >= W / 8 ? 0x80000000u
-                                  : (uint32_t)(row * st * sizeof(in_t) + 16 * (pg ^ TileL<W>::swz(row)));
+            const int sg = pg ^ TileL<W>::swz(row);  // source granule at this position
+            voff[j] = pg >= W / 8 || sg >= SRCW / 8 ? 0x80000000u : (uint32_t)(row * st * sizeof(in_t) + 16 * sg);
         }
     }
     // Rows [t0, t0 + 64) into `tile` (row t0 + i at tile row i).
