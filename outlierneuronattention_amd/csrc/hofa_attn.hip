@@ -108,21 +108,17 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
     __shared__ __attribute__((aligned(16))) uint32_t sV[2][D * VTP];
     __shared__ float sKn[2][BN];  // squared norm of every key row of each tile
 
-    // Each block runs two row blocks of one head, qb = nq - 1 - j and then
-    // qb = j: every pair holds the same causal work, so all blocks finish
-    // together (one round of blocks, no tail of short ones).
+    // One row block per block, dispatched longest first (row block nq - 1 has
+    // the most causal work): the blocks that start last are the short ones,
+    // and they fill the CUs that the long ones leave free.
     const int nq = (a.T + BM - 1) / BM;
-    const int npair = (nq + 1) / 2;
-    int bh, pj;
-    xcd_remap(blockIdx.x, npair, a.B * a.H, &bh, &pj);
+    int bh, rank;
+    xcd_rank_remap(blockIdx.x, nq, a.B * a.H, &bh, &rank);
     const int b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hi = lane >> 5;  // which half of the wave
-    const int nrun = pj < nq - 1 - pj ? 2 : 1;
-#pragma nounroll
-    for (int run = 0; run < nrun; ++run) {  // the LDS tiles of the first were last read before its final barrier
-    const int qb = run == 0 ? nq - 1 - pj : pj;
+    const int qb = nq - 1 - rank;
     const int q0 = qb * BM;
     const int qw0 = q0 + 32 * w;  // first query row of this wave
     const int qrow = qw0 + (lane & 31);
@@ -344,7 +340,7 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
 
     // ---- epilogue: y (+)= mix * O, optional O and lse
     const float l = xor32_sum(lsum);
-    if (qrow >= a.T) continue;
+    if (qrow >= a.T) return;
     const float inv = 1.f / l;
     const float mixv = a.mix ? load_any(a.mix, a.mix_dt, b * a.m_sb + h * a.m_sh + (int64_t)qrow * a.m_st) : 1.f;
     in_t *yr = (in_t *)a.y + b * a.y_sb + h * a.y_sh + (int64_t)qrow * a.y_st;
@@ -387,13 +383,12 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
             }
         }
     if (a.lse && hi == 0) a.lse[(int64_t)bh * a.T + qrow] = mref + __log2f(l);
-    }
 }
 
 template <int DT, int R, int D>
 void launch(const AttnFwdK &k, hipStream_t s) {
     const int nq = (k.T + BM - 1) / BM;
-    hipLaunchKernelGGL((attn_fwd_kernel<DT, R, D>), dim3((nq + 1) / 2 * k.B * k.H), dim3(NT), 0, s, k);
+    hipLaunchKernelGGL((attn_fwd_kernel<DT, R, D>), dim3(nq * k.B * k.H), dim3(NT), 0, s, k);
 }
 
 template <int DT>

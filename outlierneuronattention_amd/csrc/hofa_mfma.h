@@ -162,25 +162,11 @@ __device__ __forceinline__ u32x4 bload_op8(__amdgpu_buffer_rsrc_t r, uint32_t of
     }
 }
 
-// Block-index remap that keeps all blocks of one head on one XCD (blocks are
-// dispatched round-robin over 8 XCDs) and walks each head's row blocks from
-// the last to the first (longest causal rows first).
-__device__ __forceinline__ void xcd_remap(int blk, int nrow, int nhead, int *head, int *rowblk) {
-    constexpr int kXcd = 8;
-    if (nhead % kXcd == 0) {
-        const int xcd = blk % kXcd, slot = blk / kXcd;
-        *head = (slot / nrow) * kXcd + xcd;
-        *rowblk = nrow - 1 - slot % nrow;
-    } else {
-        *head = blk / nrow;
-        *rowblk = nrow - 1 - blk % nrow;
-    }
-}
-
-// Longest-first variant for kernels whose blocks carry unequal causal work:
-// blocks of one head stay on one XCD, and each XCD takes the work rank
-// (0 = most work) as the outer index over its heads, so every XCD dispatches
-// all of its longest blocks before any shorter one.
+// Block-index remap for kernels whose blocks carry unequal causal work.
+// Blocks are dispatched round-robin over 8 XCDs; all blocks of one head stay
+// on one XCD (its L2 holds the head's keys and values), and each XCD takes the
+// work rank (0 = most work) as the outer index over its heads, so every XCD
+// dispatches all of its longest blocks before any shorter one.
 __device__ __forceinline__ void xcd_rank_remap(int blk, int nrank, int nhead, int *head, int *rank) {
     constexpr int kXcd = 8;
     if (nhead % kXcd == 0) {
