@@ -10,8 +10,9 @@
 //   P = exp2(c S - m)                       c = sm_scale log2 e; each lane owns one query row
 //                                           (its 16 scores of the half sit in its registers and
 //                                           in lane l^32), m = the row's reference max
-//   O^T[dv, query] += V_half^T P^T          A = V^T from LDS (stored transposed), B = P straight
-//                                           from the score registers (keys permuted consistently)
+//   O^T[dv, query] += V_half^T P^T          A = V^T read from the row-major V tile with the
+//                                           transposing LDS load, B = P straight from the score
+//                                           registers (keys in the order the load delivers them)
 //   l[query] += sum P                       dot2 of the packed 16-bit P with (1, 1): the row sum
 //                                           of the same rounded P that enters O (f32 inputs: an
 //                                           exact f32 sum of the unrounded P)
@@ -22,21 +23,21 @@
 // row max at all when the Cauchy-Schwarz bound c |q| |k| (the key norms are
 // taken while the tile is staged) is within m + kTau for every key of the tile
 // and every row of the wave.
-// K (row-major) and V^T tiles are double-buffered in LDS; the next tile's
+// K and V tiles are double-buffered in LDS, both row-major; the next tile's
 // range-checked buffer loads are in flight while the current tile is consumed.
-// V^T rows hold their 64 keys in operand order (each 16-byte group is the 8
-// keys one lane's operand takes) at a pitch of 36 dwords, and each half-wave
-// of the transposing stores covers the 32 key pairs of one 16-byte column:
-// both the stores and the 16-byte operand reads are free of bank conflicts.
+// K goes through registers (its squared row norms, v_dot2 of the packed
+// operand with itself, are taken on the way); 16-bit V is written to LDS by
+// the loads themselves (LDS DMA) in the swizzled 16-byte-granule layout whose
+// row reads and transposing reads are free of bank conflicts, f32 V is
+// rounded to bf16 in registers first.
 #include <type_traits>
 
-#include "hofa_mfma.h"
+#include "hofa_tile.h"
 
 namespace hofa {
 namespace {
 
 constexpr int BM = 128, BN = 64, NT = 256;
-constexpr int VTP = 36;  // V^T row pitch in dwords (64 keys + 8 pad bf16)
 
 struct AttnFwdK {
     const void *q, *k, *v, *mix;
@@ -85,10 +86,15 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
-// Position of key `key` (0..63 within a tile) in its V^T row: bits 2 and 3 of
-// the key swap, so keys {4h..4h+3, 8+4h..8+4h+3} of each 16-key step (the
-// operand of the lanes with hi = h) form one 16-byte group.
-__device__ __forceinline__ int vt_pos(int key) { return (key & ~0xC) | ((key >> 1) & 4) | ((key << 1) & 8); }
+// acc + |x|^2 for a dword of two 16-bit key elements (v_dot2 of x with itself).
+template <int DT>
+__device__ __forceinline__ float dot2_self(uint32_t x, float acc) {
+    if constexpr (kF16Ops<DT>)
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x), __builtin_bit_cast(f16x2, x), acc, false);
+    else
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x), __builtin_bit_cast(bf16x2, x), acc,
+                                               false);
+}
 
 template <int DT, int R, int D>
 __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_kernel(AttnFwdK a) {
@@ -98,14 +104,11 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
     constexpr int KP = R + 8;        // K tile pitch in LDS (elements)
     constexpr int KCH = BN * R / 8;  // 16-byte K chunks per tile
     constexpr int NKC = (KCH + NT - 1) / NT;
-    constexpr int CPR = D / 8;                  // 16-byte chunks per V row
-    constexpr int NVP = (BN / 2) * CPR / NT;    // (2 keys x 8 dv) pieces of V per thread
-    static_assert(NVP >= 1 && (BN / 2) * CPR % NT == 0, "V tile split");
     constexpr bool SPLIT = DT == HOFA_F32;      // logits from split-bf16 operands
     constexpr int KLO = SPLIT ? BN * KP : 0;    // offset of the K remainder tile
     constexpr float kTau = kF16Ops<DT> ? 15.f : 64.f;  // P <= 2^kTau (f16 operands: below 65504)
     __shared__ __attribute__((aligned(16))) uint16_t sK[2][BN * KP + KLO];
-    __shared__ __attribute__((aligned(16))) uint32_t sV[2][D * VTP];
+    __shared__ __attribute__((aligned(16))) uint16_t sV[2][tile::TileL<D>::ELEMS];  // V row-major, keys = rows
     __shared__ float sKn[2][BN];  // squared norm of every key row of each tile
 
     // One row block per block, dispatched longest first (row block nq - 1 has
@@ -154,11 +157,19 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
     // ---- cooperative tile loader (global -> registers -> LDS): the next tile's
     // loads are in flight while the current tile is consumed
     u32x4 kreg[NKC], klo[NKC];
-    u32x4 vreg[NVP][2];
+    // V: 16-bit inputs by LDS DMA straight into the tile image, f32 inputs
+    // through registers (rounded to the bf16 operand)
+    constexpr bool VDMA = DT != HOFA_F32;
+    tile::TileDma<D> vdma;
+    tile::TileStage<DT, D, false> vstage;
+    if constexpr (VDMA) vdma.init(vp, a.v_st, a.T, w, lane);
+    int vtr[MB][2];  // lane offsets of the transposing V^T operand reads
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) vtr[mb][j] = tile::tr_lane_off<D>(32 * mb, lane, j);
     constexpr int ES = sizeof(in_t);
     const __amdgpu_buffer_rsrc_t rk = rows_rsrc(kp, (uint32_t)(a.T * a.k_st * ES));
-    const __amdgpu_buffer_rsrc_t rv = rows_rsrc(vp, (uint32_t)(a.T * a.v_st * ES));
-    // V piece pi: key pair kp = pi % 32 (rows 2kp, 2kp + 1) x 16-byte column cch = pi / 32
     auto gload = [&](int kt) {
         const int k0 = kt * BN;
 #pragma unroll
@@ -168,13 +179,8 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
             const uint32_t off = (uint32_t)(((k0 + row) * a.k_st + 8 * part) * ES);
             kreg[i] = bload_op8<DT>(rk, off, SPLIT ? &klo[i] : nullptr);
         }
-#pragma unroll
-        for (int i = 0; i < NVP; ++i) {
-            const int pi = tid + NT * i, kpair = pi % 32, cch = pi / 32;
-            const uint32_t off = (uint32_t)(((k0 + 2 * kpair) * a.v_st + 8 * cch) * ES);
-            vreg[i][0] = bload_op8<DT>(rv, off);
-            vreg[i][1] = bload_op8<DT>(rv, off + (uint32_t)(a.v_st * ES));
-        }
+        if constexpr (VDMA) vdma.fetch(sV[kt & 1], k0, w);
+        else vstage.fetch(vp, a.v_st, k0, a.T);
     };
     auto lstore = [&](int buf) {
 #pragma unroll
@@ -183,12 +189,13 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
             float ss = 0.f;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                float x0 = op_to_f32<DT>(kreg[i][e] & 0xffffu), x1 = op_to_f32<DT>(kreg[i][e] >> 16);
                 if constexpr (SPLIT) {
-                    x0 += op_to_f32<DT>(klo[i][e] & 0xffffu);
-                    x1 += op_to_f32<DT>(klo[i][e] >> 16);
+                    const float x0 = op_to_f32<DT>(kreg[i][e] & 0xffffu) + op_to_f32<DT>(klo[i][e] & 0xffffu);
+                    const float x1 = op_to_f32<DT>(kreg[i][e] >> 16) + op_to_f32<DT>(klo[i][e] >> 16);
+                    ss = fmaf(x0, x0, fmaf(x1, x1, ss));
+                } else {
+                    ss = dot2_self<DT>(kreg[i][e], ss);
                 }
-                ss = fmaf(x0, x0, fmaf(x1, x1, ss));
             }
             ss = group_sum<R / 8>(ss);  // the row's chunks sit in R/8 consecutive lanes
             if (ci < KCH) {
@@ -198,18 +205,8 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
                 if constexpr (SPLIT) *(u32x4 *)&sK[buf][KLO + row * KP + 8 * part] = klo[i];
             }
         }
-#pragma unroll
-        for (int i = 0; i < NVP; ++i) {
-            const int pi = tid + NT * i, kpair = pi % 32, cch = pi / 32;
-            uint32_t *dst = &sV[buf][8 * cch * VTP + (vt_pos(2 * kpair) >> 1)];
-            // transpose a (2 keys x 8 dv) piece: dv row gets the key pair as one dword
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t x0 = vreg[i][0][e], x1 = vreg[i][1][e];
-                dst[(2 * e) * VTP] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
-                dst[(2 * e + 1) * VTP] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
-            }
-        }
+        if constexpr (!VDMA) vstage.put(sV[buf], nullptr);
+        else tile::wait_vmem();  // this wave's share of the V tile has landed
     };
 
     float mref = -INFINITY;  // reference max of the scaled logits (base 2)
@@ -275,7 +272,9 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
             }
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
-                const u32x4 va = *(const u32x4 *)&sV[buf][(32 * mb + (lane & 31)) * VTP + 4 * (2 * ks4 + hi)];
+                const uint16_t *vt = sV[buf] + 16 * ks4 * tile::TileL<D>::PITCH;  // V^T operand (tr_operand)
+                const uint2 v0 = tile::lds_tr16(vt + vtr[mb][0]), v1 = tile::lds_tr16(vt + vtr[mb][1]);
+                const u32x4 va = {v0.x, v0.y, v1.x, v1.y};
                 o[mb] = mfma32<DT>(va, pb, o[mb]);
             }
         }

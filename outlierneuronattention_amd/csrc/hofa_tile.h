@@ -77,6 +77,17 @@ __device__ __forceinline__ u32x4 tr_operand_lin(const uint16_t *tile, int krow0,
     return u32x4{a.x, a.y, b.x, b.y};
 }
 
+// The two LDS reads of tr_operand<W>(tile, krow0, col0, lane) are at
+// tile + krow0 * PITCH + tr_lane_off<W>(col0, lane, j), j = 0, 1 (krow0 a
+// multiple of 16): loops that read many operands of one tile keep these
+// per-lane offsets in registers instead of recomputing the swizzle.
+template <int W>
+__device__ __forceinline__ int tr_lane_off(int col0, int lane, int j) {
+    const int g = lane >> 4, s = lane & 15;
+    const int i0 = W >= 32 ? 16 * (g & 1) : 0;
+    return TileL<W>::off(4 * (g >> 1) + (s >> 2) + 8 * j, col0 + i0 + 4 * (s & 3));
+}
+
 // Rows [t0, t0+64) of a [T, W] input matrix, staged global -> registers
 // (fetch, issued a tile ahead) -> LDS (put) as row-major 16-bit operands in the
 // TileL<W> layout, rows past T zero; f32 inputs also keep their bf16 rounding
@@ -150,7 +161,8 @@ struct TileDma {
         for (int j = 0; j < NW; ++j) {
             const int i = 4 * j + wave;
             if (NLOAD % 4 != 0 && i >= NLOAD) break;
-            const uint32_t off = voff[j] == 0x80000000u ? voff[j] : voff[j] + base;
+            constexpr bool kPad = TileL<W>::PITCH != W || SRCW != W;  // some lanes fetch padding
+            const uint32_t off = !kPad || voff[j] != 0x80000000u ? voff[j] + base : voff[j];
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(tile + 512 * i),
                                                      16, off, 0, 0, 0);
         }
