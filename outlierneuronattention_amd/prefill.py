@@ -7,6 +7,9 @@ then ``exact_attention_triton`` adds ``mix * softmax-attention`` into the same
 bf16 buffer) with one difference in rounding: the GLA result is handed to the
 attention kernel in float32 and the sum is rounded to the output dtype once,
 where the reference rounds the GLA part to bf16 first and the sum again.
+The second rounding would cost the stated bf16 bar: at cfg2 (outputs up to
+about 4, half a bf16 ulp 0.016 there) two roundings reach 0.027 max-abs
+against the float32 oracle, above 2e-2.
 """
 from __future__ import annotations
 
