@@ -68,10 +68,12 @@ int validate(const hofa_gla_bwd_args_t *a) {
                      "hofa_gla_bwd: o and dout_attn need the dtype of q and aligned rows");
     }
     HOFA_REQUIRE((a->R * es) % 16 == 0, HOFA_EINVAL, "hofa_gla_bwd: the inlier columns must start 16-byte aligned");
-    for (const hofa_view_t *v : {&a->q, &a->k, &a->v})
+    for (const hofa_view_t *v : {&a->q, &a->k, &a->v, &a->dy, &a->n, &a->o}) {
+        if (!v->data) continue;
         HOFA_REQUIRE((int64_t)(a->T + 2 * C) * v->stride[2] * es < (1ll << 31) &&
                          (int64_t)(a->T + 2 * C) * a->D * es < (1ll << 31),
                      HOFA_EUNSUPPORTED, "hofa_gla_bwd: one head's rows must span less than 2 GiB");
+    }
     HOFA_REQUIRE(a->rstd && a->chunk_states && ((uintptr_t)a->chunk_states % 16) == 0, HOFA_EINVAL,
                  "hofa_gla_bwd: rstd and 16-byte aligned chunk_states from the forward are required");
     HOFA_REQUIRE(a->gla_scale.data && a->d_gla_scale.data, HOFA_EINVAL, "hofa_gla_bwd: gla_scale and d_gla_scale are required");

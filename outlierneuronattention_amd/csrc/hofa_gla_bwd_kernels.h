@@ -75,28 +75,6 @@ struct GlaBwdK {
     int ntile;
 };
 
-// 8 consecutive elements of row t starting at column col, as floats (0 past T).
-template <int DT>
-__device__ __forceinline__ void row8f(const typename Stor<DT>::type *base, int64_t st, int t, int T, int col,
-                                      float *x) {
-    if (t < T) {
-        const typename Stor<DT>::type *p = base + (int64_t)t * st + col;
-        if constexpr (DT == HOFA_F32) {
-            const f32x4 u = *(const f32x4 *)p, v = *(const f32x4 *)(p + 4);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[e] = u[e];
-                x[4 + e] = v[e];
-            }
-        } else {
-            unpack16<DT>(*(const u32x4 *)p, x);
-        }
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = 0.f;
-    }
-}
-
 template <int DT>
 __device__ __forceinline__ void store8(typename Stor<DT>::type *p, const float *x) {
     if constexpr (DT == HOFA_F32) {
@@ -140,20 +118,40 @@ __global__ __launch_bounds__(256) void gla_bwd_epilogue_kernel(GlaBwdK a) {
         for (int off = LPR / 2; off >= 1; off >>= 1) x += __shfl_xor(x, off);
         return x;
     };
+    // The rows of pass p + 1 are loaded while pass p is computed and stored
+    // (range-checked buffer loads: rows past T read as zeros).
+    const Rows<DT> dyr((const in_t *)a.dy + b * a.dy_sb + h * a.dy_sh, a.dy_st, T);
+    const Rows<DT> nr((const in_t *)a.n + b * a.n_sb + h * a.n_sh, a.n_st, T);
+    const Rows<DT> orw(a.o ? (const in_t *)a.o + b * a.o_sb + h * a.o_sh : (const in_t *)a.dy, a.o ? a.o_st : 0,
+                       a.o ? T : 0);
+    struct Pass {
+        Raw8<DT> y, n, o;
+        float m, rs;
+    };
+    auto fetch = [&](int t, Pass &p) {
+        p.y.load(dyr, t, d0);
+        p.n.load(nr, t, d0);
+        if (a.o) p.o.load(orw, t, d0);
+        p.m = a.f.mix && t < T ? load_any(a.f.mix, a.f.mix_dt, b * a.f.m_sb + h * a.f.m_sh + (int64_t)t * a.f.m_st)
+                               : 0.f;
+        p.rs = t < T ? a.rstd[(int64_t)bh * T + t] : 0.f;
+    };
+    Pass cur, nxt;
+    fetch(tile * ET + r, cur);
     for (int pass = 0; pass < ET / RPP; ++pass) {
         const int t = tile * ET + pass * RPP + r;
         if (t >= T) break;  // whole row groups leave together
+        if (pass + 1 < ET / RPP) fetch(t + RPP, nxt);
         float dy[8], nv[8], ov[8];
-        row8f<DT>((const in_t *)a.dy + b * a.dy_sb + h * a.dy_sh, a.dy_st, t, T, d0, dy);
-        row8f<DT>((const in_t *)a.n + b * a.n_sb + h * a.n_sh, a.n_st, t, T, d0, nv);
+        cur.y.get(dy);
+        cur.n.get(nv);
         if (a.o) {
-            row8f<DT>((const in_t *)a.o + b * a.o_sb + h * a.o_sh, a.o_st, t, T, d0, ov);
+            cur.o.get(ov);
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e) ov[e] = 0.f;
         }
-        const float m = a.f.mix ? load_any(a.f.mix, a.f.mix_dt, b * a.f.m_sb + h * a.f.m_sh + (int64_t)t * a.f.m_st) : 0.f;
-        const float rs = a.rstd[(int64_t)bh * T + t];
+        const float m = cur.m, rs = cur.rs;
         float dn[8], snn = 0.f, syo = 0.f, syn = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -181,6 +179,7 @@ __global__ __launch_bounds__(256) void gla_bwd_epilogue_kernel(GlaBwdK a) {
             if (a.delta) a.delta[(int64_t)bh * T + t] = m * syo;
             if (a.dmix) store_any(a.dmix, a.dmix_dt, b * a.dmix_sb + h * a.dmix_sh + (int64_t)t * a.dmix_st, syo - syn);
         }
+        cur = nxt;
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) sP[tid][e] = part[e];
