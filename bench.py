@@ -276,13 +276,35 @@ def bench_train(steps: int, warmup: int):
     torch.cuda.synchronize()
     ms = ev[0].elapsed_time(ev[1]) / steps
     ms_fwd = ev[1].elapsed_time(ev[2]) / steps
+    # The same step (forward and backward, gradients into static tensors) captured
+    # in one HIP graph and replayed: the launch gaps of the eager autograd step go.
+    graph = torch.cuda.CUDAGraph()
+    for t in inp.values():
+        t.grad = None
+    with torch.cuda.graph(graph):
+        _train_step(inp, dy, backward=False).backward(dy)
+    graph.replay()
+    torch.cuda.synchronize()
+    gs = torch.cuda.current_stream()
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g0.record(gs)
+    for _ in range(steps):
+        graph.replay()
+    g1.record(gs)
+    torch.cuda.synchronize()
+    ms_graph = g0.elapsed_time(g1) / steps
+    del graph
     fwd, bwd = train_flops()
     tfs = (fwd + bwd) / (ms * 1e-3) / 1e12
+    tfs_graph = (fwd + bwd) / (ms_graph * 1e-3) / 1e12
     return dict(workload="cfg4: attention core fwd+bwd, B=8 T=2048 H=12 d_h=64 r=16 (j=48), learnable "
                          "per-channel decay, bf16 operands, fp32 decay/gate grads (projections excluded)",
                 ms_per_step=round(ms, 4), ms_fwd_only=round(ms_fwd, 4), gflop=round((fwd + bwd) / 1e9, 2),
                 tflops=round(tfs, 1), mfma_frac=round(tfs / MFMA_BF16_PEAK_TFS, 4),
-                timing="eager launches (autograd), HIP events on the current stream")
+                timing="eager launches (autograd), HIP events on the current stream",
+                ms_per_step_graph=round(ms_graph, 4), tflops_graph=round(tfs_graph, 1),
+                mfma_frac_graph=round(tfs_graph / MFMA_BF16_PEAK_TFS, 4),
+                timing_graph="the same forward+backward step captured in one HIP graph, replayed")
 
 
 # ---------------------------------------------------------------- full model (cfg5)
