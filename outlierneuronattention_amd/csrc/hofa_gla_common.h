@@ -121,10 +121,19 @@ struct Raw8 {
     }
 };
 
+// Token-granule swizzle of a transposed tile: element (row, t) at
+// row * PITCH + ((t / 8) ^ tr_swz(row)) * 8 + t % 8.  With PITCH = 8 (mod 16),
+// a commit's 4-byte stores to rows eight channels apart (a [64][PITCH] tile
+// store pass) fall on distinct banks instead of four rows per bank, and reads
+// of 16 consecutive rows at one token granule (tr_swz constant over them)
+// stay conflict-free.
+__device__ __forceinline__ int tr_swz(int row) { return 2 * ((row >> 4) & 3); }
+
 // A [C x W] chunk tile (columns [col0, col0+W)) in pieces of 2 rows x 8
 // columns per thread, committed to LDS transposed ([W][PITCH] 16-bit
-// operands, tokens contiguous); rows past T are zero.
-template <int DT, int W, int NTH>
+// operands, tokens contiguous, token granules swizzled by tr_swz when SWZ);
+// rows past T are zero.
+template <int DT, int W, int NTH, bool SWZ = false>
 struct TrStage {
     static constexpr int NPIECE = (C / 2) * (W / 8);
     static constexpr int PT = (NPIECE + NTH - 1) / NTH;
@@ -159,11 +168,13 @@ struct TrStage {
                 }
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
+                    const int row = 8 * cc + e;
+                    const int o = SWZ ? row * PITCH + (((t >> 3) ^ tr_swz(row)) << 3) + (t & 7) : row * PITCH + t;
                     const uint32_t hv = pack2<OPB>(x[0][e], x[1][e]);
-                    *(uint32_t *)&dst[(8 * cc + e) * PITCH + t] = hv;
+                    *(uint32_t *)&dst[o] = hv;
                     if constexpr (LO)
-                        *(uint32_t *)&dst_lo[(8 * cc + e) * PITCH + t] = pack2<OPB>(
-                            x[0][e] - op_to_f32<OPB>(hv & 0xffffu), x[1][e] - op_to_f32<OPB>(hv >> 16));
+                        *(uint32_t *)&dst_lo[o] = pack2<OPB>(x[0][e] - op_to_f32<OPB>(hv & 0xffffu),
+                                                             x[1][e] - op_to_f32<OPB>(hv >> 16));
                 }
             }
         }
@@ -315,8 +326,8 @@ __global__ __launch_bounds__(kStateThreads) void gla_state_kernel(GlaK a) {
     const Rows<DT> krows((const in_t *)a.k + b * a.k_sb + h * a.k_sh, a.k_st, a.T);
     const Rows<DT> vrows((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, a.T);
     DecayStage<J, GENERAL, NTH> dst;
-    TrStage<DT, J, NTH> kst;
-    TrStage<DT, D, NTH> vst;
+    TrStage<DT, J, NTH, true> kst;
+    TrStage<DT, D, NTH, true> vst;
     dst.issue(a, b, h, t0);
     kst.issue(krows, a.key_col0, t0);
     vst.issue(vrows, 0, t0);
@@ -340,9 +351,9 @@ __global__ __launch_bounds__(kStateThreads) void gla_state_kernel(GlaK a) {
         const int tm = tile / (J / 16), tn = tile % (J / 16);
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < C / 32; ++ks) {
-            const int vo = (16 * tm + r16) * TP + 32 * ks + 8 * g4;
-            const int ko = (16 * tn + r16) * TP + 32 * ks + 8 * g4;
+        for (int ks = 0; ks < C / 32; ++ks) {  // token granule 4 ks + g4 of rows 16 tm + r16 / 16 tn + r16
+            const int vo = (16 * tm + r16) * TP + (((4 * ks + g4) ^ tr_swz(16 * tm)) << 3);
+            const int ko = (16 * tn + r16) * TP + (((4 * ks + g4) ^ tr_swz(16 * tn)) << 3);
             const u32x4 av = *(const u32x4 *)&sVt[0][vo];
             acc = mfma16<OPB>(av, *(const u32x4 *)&sKt[0][ko], acc);
             if constexpr (KLO) acc = mfma16<OPB>(av, *(const u32x4 *)&sKt[KLO ? 1 : 0][ko], acc);
