@@ -61,6 +61,26 @@ __global__ __launch_bounds__(LT) void rows_linear_kernel(RowsLinK a) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int K = a.K, K8 = K / 8;
 
+    // ---- for one or two batch rows the wave's first weight pieces are
+    // requested before x is staged: they do not depend on it, so their latency
+    // overlaps the LayerNorm (with more rows the staged pieces of x fill the
+    // registers, and the early pieces would cost a wave per SIMD)
+    constexpr bool PRE = NB <= 2;
+    const int n0 = (blockIdx.x * LW + w) * RPW;
+    const st *wr[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) wr[i] = (const st *)a.w + (int64_t)min(n0 + i, a.N - 1) * K;
+    constexpr int U = 4;
+    u32x4 wv0[PRE ? RPW : 1][U];
+    if constexpr (PRE) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = min(lane + 64 * u, K8 - 1);
+#pragma unroll
+            for (int i = 0; i < RPW; ++i) wv0[i][u] = __builtin_nontemporal_load((const u32x4 *)(wr[i] + 8 * c));
+        }
+    }
+
     // ---- stage x (LayerNorm'd when ln_w is given) in LDS.  LayerNorm: every
     // 16-byte piece of the NB rows is loaded once into registers, the sums and
     // sums of squares of each row go through one block reduction, and the
@@ -173,23 +193,25 @@ __global__ __launch_bounds__(LT) void rows_linear_kernel(RowsLinK a) {
     __syncthreads();
 
     // ---- RPW rows per wave, 16-byte weight pieces, four pieces in flight per row
-    const int n0 = (blockIdx.x * LW + w) * RPW;
     float acc[RPW][NB];
 #pragma unroll
     for (int i = 0; i < RPW; ++i)
 #pragma unroll
         for (int b = 0; b < NB; ++b) acc[i][b] = 0.f;
-    const st *wr[RPW];
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) wr[i] = (const st *)a.w + (int64_t)min(n0 + i, a.N - 1) * K;
-    constexpr int U = 4;
     for (int c0 = lane; c0 < K8; c0 += 64 * U) {
         u32x4 wv[RPW][U];
+        if (PRE && c0 == lane) {  // the pieces loaded before the staging
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = min(c0 + 64 * u, K8 - 1);
+            for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int i = 0; i < RPW; ++i) wv[i][u] = __builtin_nontemporal_load((const u32x4 *)(wr[i] + 8 * c));
+                for (int i = 0; i < RPW; ++i) wv[i][u] = wv0[PRE ? i : 0][u];
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = min(c0 + 64 * u, K8 - 1);
+#pragma unroll
+                for (int i = 0; i < RPW; ++i) wv[i][u] = __builtin_nontemporal_load((const u32x4 *)(wr[i] + 8 * c));
+            }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
