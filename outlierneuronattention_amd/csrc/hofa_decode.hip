@@ -324,28 +324,6 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeKArgs a) 
     // with the prologue the newest row is the state block's partial
     const int we = min(ws + tpw, PRO ? max(seq_len - 1, 0) : seq_len);
 
-    const st *qp = (const st *)a.q + b * a.q_sb + h * a.q_sh;
-    float qv[EPV];
-#pragma unroll
-    for (int e = 0; e < EPV; ++e) qv[e] = to_f32<DT>(qp[(pk * EPV + e) * a.q_sd]);
-    if constexpr (PRO) {  // rotate this lane's q elements; the partner half sits KL/2 lanes away
-        static_assert(KL >= 2, "RoPE partner lanes");
-        if (a.rope) {
-            const int64_t prow = (int64_t)min(max(seq_len - 1, 0), a.rope_rows - 1) * R;
-            float pq[EPV];
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) pq[e] = __shfl_xor(qv[e], KL / 2);
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) {
-                const int d = pk * EPV + e;
-                qv[e] = rope1<DT>(qv[e], pq[e], pk < KL / 2, load_any(a.rcos, a.rope_dt, prow + d),
-                                  load_any(a.rsin, a.rope_dt, prow + d), a.rope_dt);
-            }
-        }
-    }
-#pragma unroll
-    for (int e = 0; e < EPV; ++e) qv[e] *= a.qscale;
-
     const st *ckh = (const st *)a.cache_k + b * a.ck_sb + h * a.ck_sh;
     const st *cvh = (const st *)a.cache_v + b * a.cv_sb + h * a.cv_sh;
     const int krow = (int)(a.ck_sl * sizeof(st)), vrow = (int)(a.cv_sl * sizeof(st));
@@ -354,11 +332,6 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeKArgs a) 
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void *)cvh, 0, nvalid * vrow, kBufFlags);
     const int koff0 = (lane / KL) * krow + pk * 16;
     const int voff0 = (lane / LPR) * vrow + pv * 16;
-
-    float m_run = -INFINITY, l_run = 0.f;
-    float acc[EPV];
-#pragma unroll
-    for (int e = 0; e < EPV; ++e) acc[e] = 0.f;
 
     u32x4 kb[NKL], vb[NVL];
     auto load_tile = [&](int t0, u32x4 *kd, u32x4 *vd) {
@@ -371,8 +344,64 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeKArgs a) 
             vd[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                   rv, voff0 + (t0 + i * (64 / LPR)) * vrow, 0, kLoadNT));
     };
-
+    // The first tile's cache rows are requested before q: they do not depend on
+    // it, and q (with the rotary rows of the prologue variant) then arrives
+    // within the same memory round trip.
     if (ws < we) load_tile(ws, kb, vb);
+
+    // raw q elements, converted only after the rotary rows are requested, so
+    // no wait for them sits between the loads
+    const st *qp = (const st *)a.q + b * a.q_sb + h * a.q_sh;
+    st qraw[EPV];
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) qraw[e] = qp[(pk * EPV + e) * a.q_sd];
+    // the prologue variant's rotary elements of this lane (one dtype test for all)
+    float cs[EPV], sn[EPV];
+    if constexpr (PRO) {
+        if (a.rope) {
+            const int64_t prow = (int64_t)min(max(seq_len - 1, 0), a.rope_rows - 1) * R + pk * EPV;
+            if (a.rope_dt == HOFA_F32) {
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) {
+                    cs[e] = ((const float *)a.rcos)[prow + e];
+                    sn[e] = ((const float *)a.rsin)[prow + e];
+                }
+            } else {
+                uint16_t cr[EPV], sr[EPV];
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) {
+                    cr[e] = ((const uint16_t *)a.rcos)[prow + e];
+                    sr[e] = ((const uint16_t *)a.rsin)[prow + e];
+                }
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) {
+                    cs[e] = a.rope_dt == HOFA_BF16 ? bf16_bits_to_f32(cr[e]) : to_f32<HOFA_F16>(cr[e]);
+                    sn[e] = a.rope_dt == HOFA_BF16 ? bf16_bits_to_f32(sr[e]) : to_f32<HOFA_F16>(sr[e]);
+                }
+            }
+        }
+    }
+
+    float qv[EPV];
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) qv[e] = to_f32<DT>(qraw[e]);
+    if constexpr (PRO) {  // rotate this lane's q elements; the partner half sits KL/2 lanes away
+        static_assert(KL >= 2, "RoPE partner lanes");
+        if (a.rope) {
+            float pq[EPV];
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) pq[e] = __shfl_xor(qv[e], KL / 2);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) qv[e] = rope1<DT>(qv[e], pq[e], pk < KL / 2, cs[e], sn[e], a.rope_dt);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) qv[e] *= a.qscale;
+
+    float m_run = -INFINITY, l_run = 0.f;
+    float acc[EPV];
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) acc[e] = 0.f;
     for (int t0 = ws; t0 < we; t0 += TT) {
         u32x4 kn[NKL], vn[NVL];
         const bool more = t0 + TT < we;
