@@ -130,26 +130,8 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
     const in_t *kp = (const in_t *)a.k + b * a.k_sb + h * a.k_sh;
     const in_t *vp = (const in_t *)a.v + b * a.v_sb + h * a.v_sh;
 
-    // B operand Q (f32 inputs: hi/lo); qn = c |q| with a relative 2^-10 margin
+    // B operand Q (f32 inputs: hi/lo), loaded once the first tile's loads are issued
     u32x4 qop[KS], qlo[KS];
-    float qss = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        qop[ks] = qrow < a.T ? load_op8<DT>(qp + (int64_t)qrow * a.q_st + 16 * ks + 8 * hi) : u32x4{0, 0, 0, 0};
-        if constexpr (SPLIT)
-            qlo[ks] = qrow < a.T ? load_lo8_f32((const float *)qp + (int64_t)qrow * a.q_st + 16 * ks + 8 * hi)
-                                 : u32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float x0 = op_to_f32<DT>(qop[ks][e] & 0xffffu), x1 = op_to_f32<DT>(qop[ks][e] >> 16);
-            if constexpr (SPLIT) {
-                x0 += op_to_f32<DT>(qlo[ks][e] & 0xffffu);
-                x1 += op_to_f32<DT>(qlo[ks][e] >> 16);
-            }
-            qss = fmaf(x0, x0, fmaf(x1, x1, qss));
-        }
-    }
-    const float qn = __builtin_amdgcn_sqrtf(xor32_sum(qss)) * (a.c * (1.f + 1.f / 1024.f));
 
     const int kend = min(a.T, q0 + BM);
     const int ntiles = (kend + BN - 1) / BN;
@@ -288,6 +270,26 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
     // in, so the waves of the block stay in step through the tile staging.
     const int nfull = min(q0 / BN, ntiles);
     gload(0);
+    // Q after the first tile's K and V requests, so all three share one memory
+    // round trip; qn = c |q| with a relative 2^-10 margin
+    float qss = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        qop[ks] = qrow < a.T ? load_op8<DT>(qp + (int64_t)qrow * a.q_st + 16 * ks + 8 * hi) : u32x4{0, 0, 0, 0};
+        if constexpr (SPLIT)
+            qlo[ks] = qrow < a.T ? load_lo8_f32((const float *)qp + (int64_t)qrow * a.q_st + 16 * ks + 8 * hi)
+                                 : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float x0 = op_to_f32<DT>(qop[ks][e] & 0xffffu), x1 = op_to_f32<DT>(qop[ks][e] >> 16);
+            if constexpr (SPLIT) {
+                x0 += op_to_f32<DT>(qlo[ks][e] & 0xffffu);
+                x1 += op_to_f32<DT>(qlo[ks][e] >> 16);
+            }
+            qss = fmaf(x0, x0, fmaf(x1, x1, qss));
+        }
+    }
+    const float qn = __builtin_amdgcn_sqrtf(xor32_sum(qss)) * (a.c * (1.f + 1.f / 1024.f));
     lstore(0);
     __syncthreads();
     // The fast run needs no row max while every key k of the tile and every row
