@@ -125,14 +125,8 @@ __global__ __launch_bounds__(NT, (dkdv_occupancy<DT, R, D>())) void attn_bwd_dkd
 
     // B operands: c K as a hi/lo pair (k = dims), so the logits come out of the
     // matrix cores in base-2 units, V (k = dv) of this lane's key, and ones
-    // for the shift k-step
+    // for the shift k-step; loaded once the first tile's loads are issued
     u32x4 kh[KS], kl[KS], vop[DKS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-        load_scaled_op8<DT>(kp + (int64_t)key * a.k_st + 16 * ks + 8 * hi, a.c, key < a.T, kh[ks], kl[ks]);
-#pragma unroll
-    for (int ks = 0; ks < DKS; ++ks)
-        vop[ks] = key < a.T ? load_op8<DT>(vp + (int64_t)key * a.v_st + 16 * ks + 8 * hi) : u32x4{0, 0, 0, 0};
     const u32x4 ones = {hi ? 0u : kOnes2<DT>, 0u, 0u, 0u};
 
     f32x16 dvt[MB], dkt[RB];
@@ -252,6 +246,14 @@ __global__ __launch_bounds__(NT, (dkdv_occupancy<DT, R, D>())) void attn_bwd_dkd
         __syncthreads();
     };
     fetch(0, k0);
+    // this lane's key operands after the first tile's requests (one memory round
+    // trip; the raw V rows before K, whose scaling waits for its load)
+#pragma unroll
+    for (int ks = 0; ks < DKS; ++ks)
+        vop[ks] = key < a.T ? load_op8<DT>(vp + (int64_t)key * a.v_st + 16 * ks + 8 * hi) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+        load_scaled_op8<DT>(kp + (int64_t)key * a.k_st + 16 * ks + 8 * hi, a.c, key < a.T, kh[ks], kl[ks]);
     put(0, k0);
     __syncthreads();
     for (int q0 = k0, buf = 0; q0 < a.T; q0 += BQ, buf ^= 1) tile(buf, q0);
@@ -325,17 +327,36 @@ __global__ __launch_bounds__(NT, (dq_occupancy<DT, R, D>())) void attn_bwd_dq_ke
     const in_t *kp = (const in_t *)a.k + b * a.k_sb + h * a.k_sh;
     const in_t *vp = (const in_t *)a.v + b * a.v_sb + h * a.v_sh;
     const in_t *op = (const in_t *)a.dO + b * a.o_sb + h * a.o_sh;
+    TileStage<DT, R> stk;
+    TileStage<DT, D> stv;
+    TileDma<R> dmk;
+    TileDma<D> dmv;
+    if constexpr (!SPL) {
+        dmk.init(kp, a.k_st, a.T, w, lane);
+        dmv.init(vp, a.v_st, a.T, w, lane);
+    }
+    const int kend = min(a.T, q0 + BM);
+    // the first tile's requests go out before the per-lane operands below, so
+    // both arrive within one memory round trip
+    if constexpr (SPL) {
+        stk.fetch(kp, a.k_st, 0, a.T);
+        stv.fetch(vp, a.v_st, 0, a.T);
+    } else {
+        dmk.fetch(sK[0], 0, w);
+        dmv.fetch(sV[0], 0, w);
+    }
+
     // B operands: c Q as a hi/lo pair (k = dims), dO (k = dv) of this lane's
     // query, and the shift k-step (-lse, -Dt) against ones
     u32x4 qh[KS], ql[KS], oop[DKS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-        load_scaled_op8<DT>(qp + (int64_t)qrow * a.q_st + 16 * ks + 8 * hi, a.c, qrow < a.T, qh[ks], ql[ks]);
 #pragma unroll
     for (int ks = 0; ks < DKS; ++ks)
         oop[ks] = qrow < a.T ? load_op8<DT>(op + (int64_t)qrow * a.o_st + 16 * ks + 8 * hi) : u32x4{0, 0, 0, 0};
     const float lq = qrow < a.T ? a.lse[(int64_t)bh * a.T + qrow] : 0.f;
     const float dq_t = qrow < a.T ? a.dt[(int64_t)bh * a.T + qrow] : 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+        load_scaled_op8<DT>(qp + (int64_t)qrow * a.q_st + 16 * ks + 8 * hi, a.c, qrow < a.T, qh[ks], ql[ks]);
     const u32x4 xb = {hi ? 0u : split_pair<DT>(-lq), 0u, 0u, 0u};
     const u32x4 yb = {hi ? 0u : split_pair<DT>(-dq_t), 0u, 0u, 0u};
     const u32x4 ones = {hi ? 0u : kOnes2<DT>, 0u, 0u, 0u};
@@ -346,23 +367,10 @@ __global__ __launch_bounds__(NT, (dq_occupancy<DT, R, D>())) void attn_bwd_dq_ke
 #pragma unroll
         for (int v = 0; v < 16; ++v) dqt[rb][v] = 0.f;
 
-    TileStage<DT, R> stk;
-    TileStage<DT, D> stv;
-    TileDma<R> dmk;
-    TileDma<D> dmv;
-    if constexpr (!SPL) {
-        dmk.init(kp, a.k_st, a.T, w, lane);
-        dmv.init(vp, a.v_st, a.T, w, lane);
-    }
-    const int kend = min(a.T, q0 + BM);
     if constexpr (SPL) {
-        stk.fetch(kp, a.k_st, 0, a.T);
-        stv.fetch(vp, a.v_st, 0, a.T);
         stk.put(sK[0], sKlo[0]);
         stv.put(sV[0], nullptr);
     } else {
-        dmk.fetch(sK[0], 0, w);
-        dmv.fetch(sV[0], 0, w);
         wait_vmem();
     }
     __syncthreads();
