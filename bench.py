@@ -181,6 +181,18 @@ def _prefill_call(inp, y):
                 g=inp["g"], eps=1e-5, out=y)
 
 
+def _warm_clocks(run, sync, seconds: float = 0.2):
+    """Repeat `run` for at least `seconds` of wall time: the GPU's clocks ramp
+    up over the first tens of milliseconds of sustained work (a cfg2 attention
+    call measured 190 us at first, 165 us once settled), so the timed region
+    starts at steady state."""
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(4):
+            run()
+        sync()
+
+
 def bench_prefill(steps: int, warmup: int):
     gen = torch.Generator().manual_seed(4321)
     inp = make_prefill_inputs(gen)
@@ -196,6 +208,7 @@ def bench_prefill(steps: int, warmup: int):
             _prefill_call(inp, y)
         g.replay()
         s.synchronize()
+        _warm_clocks(g.replay, s.synchronize)
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0.record(s)
         for _ in range(steps):
@@ -262,6 +275,7 @@ def bench_train(steps: int, warmup: int):
     inp, dy = make_train_inputs(gen)
     for _ in range(max(2, warmup)):
         _train_step(inp, dy)
+    _warm_clocks(lambda: _train_step(inp, dy), torch.cuda.synchronize)
     torch.cuda.synchronize()
     s = torch.cuda.current_stream()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
