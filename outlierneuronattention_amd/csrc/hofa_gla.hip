@@ -120,7 +120,7 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
 
     // ---- issue every load of the chunk
     DecayStage<J, GENERAL, NT> dst;
-    TrStage<DT, D, NT> vst;
+    TrStage<DT, D, NT, 2> vst;
     dst.issue(a, b, h, t0);
     vst.issue(vrows, 0, t0);
     Raw8<DT> qr[KS], kr[KS];  // this lane's query row and key row (both 32 w + lane%32)
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(NT) void gla_out_kernel(GlaK a) {
             const int ks4 = 2 * kb + k2;
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
-                const int vo = (32 * mb + (lane & 31)) * VP + 16 * ks4 + 4 * hi;
+                const int vo = (32 * mb + (lane & 31)) * VP + ((16 * ks4 + 4 * hi) ^ tr_col_swz(32 * mb));
                 const uint2 lo = *(const uint2 *)&sVt[0][vo], hi8 = *(const uint2 *)&sVt[0][vo + 8];
                 const u32x4 va = {lo.x, lo.y, hi8.x, hi8.y};
                 y[mb] = mfma32<OPB>(va, ph, y[mb]);

@@ -129,11 +129,17 @@ struct Raw8 {
 // stay conflict-free.
 __device__ __forceinline__ int tr_swz(int row) { return 2 * ((row >> 4) & 3); }
 
+// Column swizzle of the transposed V tile of gla_out_kernel (PITCH = 4 mod
+// 16): token t of row r at column t ^ (16 if r % 64 >= 32), so the commit
+// stores of rows 32 channels apart fall on different banks; the output
+// kernel's 8-byte operand reads of 32 consecutive rows stay conflict-free.
+__device__ __forceinline__ int tr_col_swz(int row) { return ((row >> 5) & 1) << 4; }
+
 // A [C x W] chunk tile (columns [col0, col0+W)) in pieces of 2 rows x 8
 // columns per thread, committed to LDS transposed ([W][PITCH] 16-bit
-// operands, tokens contiguous, token granules swizzled by tr_swz when SWZ);
-// rows past T are zero.
-template <int DT, int W, int NTH, bool SWZ = false>
+// operands, tokens contiguous); rows past T are zero.  SWZ = 1: token
+// granules swizzled by tr_swz; SWZ = 2: columns swizzled by tr_col_swz.
+template <int DT, int W, int NTH, int SWZ = 0>
 struct TrStage {
     static constexpr int NPIECE = (C / 2) * (W / 8);
     static constexpr int PT = (NPIECE + NTH - 1) / NTH;
@@ -169,7 +175,9 @@ struct TrStage {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int row = 8 * cc + e;
-                    const int o = SWZ ? row * PITCH + (((t >> 3) ^ tr_swz(row)) << 3) + (t & 7) : row * PITCH + t;
+                    const int o = SWZ == 1   ? row * PITCH + (((t >> 3) ^ tr_swz(row)) << 3) + (t & 7)
+                                  : SWZ == 2 ? row * PITCH + (t ^ tr_col_swz(row))
+                                             : row * PITCH + t;
                     const uint32_t hv = pack2<OPB>(x[0][e], x[1][e]);
                     *(uint32_t *)&dst[o] = hv;
                     if constexpr (LO)
@@ -326,8 +334,8 @@ __global__ __launch_bounds__(kStateThreads) void gla_state_kernel(GlaK a) {
     const Rows<DT> krows((const in_t *)a.k + b * a.k_sb + h * a.k_sh, a.k_st, a.T);
     const Rows<DT> vrows((const in_t *)a.v + b * a.v_sb + h * a.v_sh, a.v_st, a.T);
     DecayStage<J, GENERAL, NTH> dst;
-    TrStage<DT, J, NTH, true> kst;
-    TrStage<DT, D, NTH, true> vst;
+    TrStage<DT, J, NTH, 1> kst;
+    TrStage<DT, D, NTH, 1> vst;
     dst.issue(a, b, h, t0);
     kst.issue(krows, a.key_col0, t0);
     vst.issue(vrows, 0, t0);
