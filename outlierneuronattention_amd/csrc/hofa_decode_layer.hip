@@ -52,7 +52,7 @@ __device__ __forceinline__ uint32_t order_key(float f) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-template <int DT, int NB, int RPW>
+template <int DT, int NB, int RPW, int KMAX>
 __global__ __launch_bounds__(LT) void rows_linear_kernel(RowsLinK a) {
     using st = typename Stor<DT>::type;
     extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [NB][K] in the storage type
@@ -65,7 +65,7 @@ __global__ __launch_bounds__(LT) void rows_linear_kernel(RowsLinK a) {
     // requested before x is staged: they do not depend on it, so their latency
     // overlaps the LayerNorm (with more rows the staged pieces of x fill the
     // registers, and the early pieces would cost a wave per SIMD)
-    constexpr bool PRE = NB <= 2;
+    constexpr bool PRE = NB <= 2 || (KMAX <= 1024 && RPW == 1);
     const int n0 = (blockIdx.x * LW + w) * RPW;
     const st *wr[RPW];
 #pragma unroll
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(LT) void rows_linear_kernel(RowsLinK a) {
     // sums of squares of each row go through one block reduction, and the
     // normalised pieces are written with 16-byte LDS stores.
     if (a.ln_w) {
-        constexpr int MAXP = (NB * 4096 / 8 + LT - 1) / LT;  // pieces per thread at K = 4096
+        constexpr int MAXP = (NB * KMAX / 8 + LT - 1) / LT;  // pieces per thread at K = KMAX
         const int np = NB * K8;
         u32x4 xp[MAXP];
         // Two passes over the register-held pieces: the mean first, then the
@@ -276,19 +276,26 @@ __global__ __launch_bounds__(LT) void rows_linear_kernel(RowsLinK a) {
     }
 }
 
-template <int DT, int NB>
-int launch_rows(const RowsLinK &k, hipStream_t s) {
+template <int DT, int NB, int KMAX>
+int launch_rows_k(const RowsLinK &k, hipStream_t s) {
     const size_t lds = (size_t)NB * k.K * 2;
     if (k.N >= 16384 || k.argmax) {  // argmax slots assume 16 rows per block
         constexpr int RPW = 4;
-        hipLaunchKernelGGL((rows_linear_kernel<DT, NB, RPW>), dim3((k.N + LW * RPW - 1) / (LW * RPW)), dim3(LT), lds,
-                           s, k);
+        hipLaunchKernelGGL((rows_linear_kernel<DT, NB, RPW, KMAX>), dim3((k.N + LW * RPW - 1) / (LW * RPW)),
+                           dim3(LT), lds, s, k);
     } else {
         constexpr int RPW = 1;
-        hipLaunchKernelGGL((rows_linear_kernel<DT, NB, RPW>), dim3((k.N + LW * RPW - 1) / (LW * RPW)), dim3(LT), lds,
-                           s, k);
+        hipLaunchKernelGGL((rows_linear_kernel<DT, NB, RPW, KMAX>), dim3((k.N + LW * RPW - 1) / (LW * RPW)),
+                           dim3(LT), lds, s, k);
     }
     return HOFA_OK;
+}
+
+// K <= 1024 (the attention and fc1 inputs of the cfg5 model) stages fewer
+// LayerNorm pieces per thread, which leaves registers for the early weight loads.
+template <int DT, int NB>
+int launch_rows(const RowsLinK &k, hipStream_t s) {
+    return k.K <= 1024 ? launch_rows_k<DT, NB, 1024>(k, s) : launch_rows_k<DT, NB, 4096>(k, s);
 }
 
 template <int DT>
