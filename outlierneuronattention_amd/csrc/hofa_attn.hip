@@ -13,9 +13,10 @@
 //   O^T[dv, query] += V_half^T P^T          A = V^T read from the row-major V tile with the
 //                                           transposing LDS load, B = P straight from the score
 //                                           registers (keys in the order the load delivers them)
-//   l[query] += sum P                       dot2 of the packed 16-bit P with (1, 1): the row sum
-//                                           of the same rounded P that enters O (f32 inputs: an
-//                                           exact f32 sum of the unrounded P)
+//   l[query] += sum P                       v_mfma_f32_16x16x32 of a 0/1 selector with the same
+//                                           packed P operand: the row sums of the rounded P that
+//                                           enters O, off the VALU (f32 inputs: an exact f32 sum
+//                                           of the unrounded P)
 // The next half's QK^T does not depend on this half's exponentials, so the
 // matrix core and the VALU can overlap.  The reference max m is set by the
 // first half and moves only when a later logit exceeds it by more than kTau
@@ -53,16 +54,6 @@ struct AttnFwdK {
     int accumulate;
     float c;  // sm_scale * log2(e)
 };
-
-// acc + p.lo + p.hi for a dword of two 16-bit probabilities (v_dot2 with (1, 1)).
-template <int DT>
-__device__ __forceinline__ float dot2_ones(uint32_t p, float acc) {
-    if constexpr (kF16Ops<DT>)
-        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), __builtin_bit_cast(f16x2, 0x3C003C00u), acc, false);
-    else
-        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p), __builtin_bit_cast(bf16x2, 0x3F803F80u),
-                                               acc, false);
-}
 
 // x(l) + x(l ^ 32) and max(x(l), x(l ^ 32)) for every lane: one
 // v_permlane32_swap of x with itself puts both halves side by side (either
@@ -197,7 +188,14 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[mb][v] = 0.f;
-    float lsum = 0.f;  // this lane's part of the row sum (the partner lane l^32 holds the rest)
+    float lsum = 0.f;  // f32 inputs: this lane's part of the row sum (the partner lane l^32 holds the rest)
+    // 16-bit P: the row sums come from the matrix core, a 16x16x32 product of
+    // a selector A (row 0: ones on k-groups 0 and 2, row 1: ones on groups 1
+    // and 3) with the packed P operand, whose k-groups 0/2 hold queries
+    // l % 16 and 1/3 queries 16 + l % 16: C[0][j] sums query j, C[1][j] query 16 + j
+    f32x4 lacc = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t selw = ((lane & 15) == ((lane >> 4) & 1) && (lane & 15) < 2) ? tile::kOnes2<DT> : 0u;
+    const u32x4 sel = {selw, selw, selw, selw};
 
     // One 32-key half (keys k0 .. k0+31, all at or before every query row of
     // the wave unless MASK).  EXACT forms the row max and moves the reference
@@ -232,7 +230,13 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
                 const float alpha = fast_exp2(mref - mn);  // 0 while O and l are still empty
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb) o[mb] *= alpha;
-                lsum *= alpha;
+                if constexpr (SPLIT) {
+                    lsum *= alpha;
+                } else {  // lacc[1] of lane j < 16 belongs to query 16 + j, whose alpha lane 16 + j holds
+                    const float a16 = __shfl(alpha, (lane & 15) + 16);
+                    lacc[0] *= alpha;
+                    lacc[1] *= a16;
+                }
                 mref = mn;
             }
         }
@@ -248,10 +252,7 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
         for (int k2 = 0; k2 < 2; ++k2) {
             const int ks4 = 2 * kb + k2;
             const u32x4 pb = pack8<DT>(s, 8 * k2);
-            if constexpr (!SPLIT) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) lsum = dot2_ones<DT>(pb[e], lsum);
-            }
+            if constexpr (!SPLIT) lacc = mfma16<DT>(sel, pb, lacc);
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const uint16_t *vt = sV[buf] + 16 * ks4 * tile::TileL<D>::PITCH;  // V^T operand (tr_operand)
@@ -340,7 +341,14 @@ __global__ __launch_bounds__(NT, (D == 64 && R <= 32) ? 4 : 2) void attn_fwd_ker
     }
 
     // ---- epilogue: y (+)= mix * O, optional O and lse
-    const float l = xor32_sum(lsum);
+    float l;
+    if constexpr (SPLIT) {
+        l = xor32_sum(lsum);
+    } else {
+        const int src = lane & 15;
+        const float l0 = __shfl(lacc[0], src), l1 = __shfl(lacc[1], src);
+        l = (lane & 16) ? l1 : l0;
+    }
     if (qrow >= a.T) return;
     const float inv = 1.f / l;
     const float mixv = a.mix ? load_any(a.mix, a.mix_dt, b * a.m_sb + h * a.m_sh + (int64_t)qrow * a.m_st) : 1.f;
