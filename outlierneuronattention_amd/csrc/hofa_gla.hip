@@ -44,7 +44,11 @@ constexpr int NT = 128;  // threads of the output kernel
 // stores.
 constexpr int kScanPF = 8;
 
-template <int DT, int D, int J>
+// NPW: the planes written per chunk (planes_written of a.nplanes), fixed at
+// compile time so the chunk loop has no branch: a branch around the stores
+// leaves the compiler's memory-counter waits conservative, and the loads of
+// the next chunks would be waited for at every chunk.
+template <int DT, int D, int J, int NPW>
 __global__ __launch_bounds__(kScanRows * J / 4) void gla_scan_kernel(GlaK a) {
     __shared__ __attribute__((aligned(16))) uint16_t sT[2][2][J * kScanPitch];
     const int bh = blockIdx.x, tid = threadIdx.x;
@@ -68,7 +72,7 @@ __global__ __launch_bounds__(kScanRows * J / 4) void gla_scan_kernel(GlaK a) {
             if (c >= nc) break;  // block-uniform
             const f32x4 d = ds[u], g = gl[u];
             fetch(u, c + kScanPF);
-            store_state_tile<DT, D, J>(a.s_in + (base + c) * a.nplanes * D * J, planes_written<D, J>(a.nplanes), dv0,
+            store_state_tile<DT, D, J>(a.s_in + (base + c) * a.nplanes * D * J, NPW, dv0,
                                        dvl, j4, S, sT[c & 1][0], sT[c & 1][1]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) S[e] = fmaf(fast_exp2(g[e] * kLog2e), S[e], d[e]);
@@ -384,7 +388,12 @@ template <int DT, int D, int J, bool GEN, bool RND>
 void launch(const GlaK &k, hipStream_t s) {
     const int nblk = k.B * k.H * k.nc;
     hipLaunchKernelGGL((gla_state_kernel<DT, D, J, GEN, false, RND>), dim3(nblk), dim3(kStateThreads), 0, s, k);
-    hipLaunchKernelGGL((gla_scan_kernel<DT, D, J>), dim3(k.B * k.H, D / kScanRows), dim3(kScanRows * J / 4), 0, s, k);
+    const dim3 sg(k.B * k.H, D / kScanRows), sb(kScanRows * J / 4);
+    switch (planes_written<D, J>(k.nplanes)) {
+        case 1: hipLaunchKernelGGL((gla_scan_kernel<DT, D, J, 1>), sg, sb, 0, s, k); break;
+        case 2: hipLaunchKernelGGL((gla_scan_kernel<DT, D, J, 2>), sg, sb, 0, s, k); break;
+        default: hipLaunchKernelGGL((gla_scan_kernel<DT, D, J, 4>), sg, sb, 0, s, k); break;
+    }
     hipLaunchKernelGGL((gla_out_kernel<DT, D, J, GEN, RND>), dim3(nblk), dim3(NT), 0, s, k);
 }
 
